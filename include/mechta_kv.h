@@ -1,0 +1,143 @@
+/*
+ * mechta_kv.h -- C ABI of the MI355X-native KV-cache path of mechta (libmechta_kv.so).
+ *
+ * One handle = the KV store of `layers` full-attention layers of one model instance: K and V per layer, 2 KV heads of
+ * head_dim 256, `ctx` positions, f16 (default) or f32. The reference keeps the same data as one K and one V wgpu
+ * buffer per layer (engine.rs:493-496, Engine.kv_buf engine.rs:240); here the store owns one HBM allocation and the
+ * layout inside it is the library's (see "Layout"). Every device pointer argument is a plain HIP device address;
+ * sizes are in elements unless named *_bytes. No call takes or returns framework types.
+ *
+ * Ordering: every call is enqueued on the handle's HIP stream (mkv_create / mkv_set_stream) and returns without
+ * waiting, except mkv_sync, mkv_snapshot (waits for the copy into host memory) and mkv_destroy. One thread per handle
+ * at a time, as the reference's engine thread (api/src/lib.rs:46).
+ *
+ * Errors: 0 = ok, a negative MKV_E_* code otherwise; mkv_last_error() returns the message of the last failure on the
+ * calling thread. The reference panics in the same situations (check_ctx engine.rs:28-33, pos + K < ctx
+ * quad.rs:278, pending-row asserts engine.rs:682/785/847); here the call is refused and nothing is enqueued.
+ *
+ * Length: the store records for each layer how many positions hold data (`len`). An append must start at or before
+ * len (no holes) and sets len = pos + ntok; attention may read positions < len only; mkv_set_len shrinks len, which
+ * is the rollback of rejected MTP drafts (the reference rolls back by starting the next step at pos + na + 1 and
+ * overwriting, quad.rs:320, session.rs:396-401: the next append here overwrites the same rows).
+ *
+ * Layout (f16): per (layer, K|V, kv head) one contiguous plane of ctx*256 halves. K planes are tiled in blocks of 32
+ * positions, [pos/32][d/8][pos%32][8]; V planes in groups of 8 positions, [pos/8][d][pos%8]. Both are the operand
+ * layouts of the CDNA4 32x32x16 f16 MFMA, so attention streams them with 16-byte loads straight into matrix operands.
+ * f32 planes are [pos][256]. mkv_read_rows / mkv_write_rows convert to and from the reference's position-major
+ * layout ([pos][kvh][256], kv.wgsl:7-8), e.g. for the reference's root files.
+ */
+#ifndef MECHTA_KV_H
+#define MECHTA_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mkv_store mkv_t;
+
+/* KV formats: KvFormat::{F16, F32} (engine.rs:49-68); MECHTA_KV=f16|f32 */
+#define MKV_F16 0
+#define MKV_F32 1
+
+/* which cache of a layer */
+#define MKV_K 0
+#define MKV_V 1
+
+#define MKV_OK 0
+#define MKV_E_ARG (-1)   /* bad argument: null pointer, ntok out of range, unknown format */
+#define MKV_E_CTX (-2)   /* ctx not a multiple of 1024 in [4096, 262144] (check_ctx, engine.rs:28-33) */
+#define MKV_E_POS (-3)   /* position range outside the store or past the written length */
+#define MKV_E_LAYER (-4) /* layer index out of range */
+#define MKV_E_SIZE (-5)  /* byte count of a snapshot buffer does not match mkv_snapshot_bytes */
+#define MKV_E_HIP (-6)   /* HIP runtime failure (message in mkv_last_error) */
+#define MKV_E_NOMEM (-7) /* device allocation failed */
+#define MKV_E_FMT (-8)   /* operation not available for this KV format */
+
+#define MKV_CTX_MIN 4096   /* engine.rs:22 */
+#define MKV_CTX_MAX 262144 /* engine.rs:23 */
+#define MKV_KV_HEADS 2
+#define MKV_Q_HEADS 16
+#define MKV_HEAD_DIM 256
+#define MKV_PREFILL_MAX 512 /* tokens per prefill block, NB (engine.rs:18) */
+
+/* Allocates the store: layers x {K, V} x 2 heads x ctx x 256 elements, zero filled, and the split-K workspaces.
+ * Replaces the per-layer KV buffer allocation (engine.rs:493-496) with the ctx check of check_ctx (engine.rs:28-33).
+ * stream: a hipStream_t (NULL = the default stream). */
+int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream);
+/* Frees everything (waits for the stream first). Replaces dropping the Engine's buffers. */
+int mkv_destroy(mkv_t* h);
+/* Changes the stream later calls are enqueued on. */
+int mkv_set_stream(mkv_t* h, void* stream);
+/* Waits for all work enqueued by this handle (the reference's device.poll(Wait)). */
+int mkv_sync(mkv_t* h);
+/* Message of the last failed call on this thread ("" if none). */
+const char* mkv_last_error(void);
+
+/* Store geometry and the recorded length of a layer. */
+int mkv_info(const mkv_t* h, int* layers, int* ctx, int* fmt);
+int mkv_len(const mkv_t* h, int layer, int* len);
+
+/* K/V append of ntok (1..512) tokens at positions pos..pos+ntok-1 of one layer.
+ *   k_normed: [ntok][2][256] f32, K after the k RMSNorm, before RoPE (device);
+ *   v:        [ntok][512] f32 (device);
+ *   rope_tab: [ntok][64] f32, rope_table(pos + t) = [cos th_0..th_31 | sin th_0..th_31] (device).
+ * K gets NEOX RoPE on dims 0..63, pairs (i, i+32), computed as a*c - b*s / a*s + b*c with every product and sum
+ * rounded to f32 (no FMA), then f32->f16 round to nearest even (f16 store) or stored as is (f32 store).
+ * Replaces kv_rope / kv_rope2 + kv_copy (kv.wgsl:19-42) and rope / rope2 + copy (ops.wgsl:141-162, 275-286). */
+int mkv_append(mkv_t* h, int layer, int pos, int ntok, const float* k_normed, const float* v, const float* rope_tab);
+
+/* Sets the length of every layer to len (len <= each layer's current length): rollback of rejected drafts. */
+int mkv_set_len(mkv_t* h, int len);
+
+/* Decode attention of ntok (1..4) query tokens of one layer, GQA 8:1, split-K over positions.
+ *   q: [ntok][16][256] f32 (device), after q RoPE; token t sees positions [start, n + t) (n = pos + 1 of token 0);
+ *   out: [ntok][16][256] f32 (device) = softmax(q.k * scale) . v per head;
+ *   gate_src: NULL, or qf [ntok][16][512] f32 (device, q | gate interleaved per head): then
+ *             out = attention * sigmoid(qf[h*512 + 256 + d]) (attn_gate, ops.wgsl:171-177).
+ * Requires n + ntok - 1 <= len(layer). Replaces attn_fd (ops.wgsl:310-394), q_dmx + attn_dmx2 (dmx.rs:19-138) and
+ * attn_fd_combine (ops.wgsl:523-538). f16 store: Q and P rounded to f16 for the matrix units, f32 sums (as attn_dmx);
+ * f32 store: f32 throughout (as attn_fd). */
+int mkv_decode(mkv_t* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
+               const float* gate_src);
+
+/* Append + decode of the same ntok tokens in one launch sequence: mkv_append(layer, n - 1, ntok, ...) followed by
+ * mkv_decode(layer, q, ntok, n, start, ...). Same results as the two calls. */
+int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* k_normed, const float* v,
+                      const float* rope_tab, const float* q, int start, float scale, float* out,
+                      const float* gate_src);
+
+/* Causal prefill attention of T (1..512) tokens of one layer: token t sees positions [start, n + t).
+ *   q: [T][16][256] f32 (device); out: [T][16][256] f32 (device); gate_src as mkv_decode ([T][16][512]).
+ * Requires n + T - 1 <= len(layer). Replaces q_f16 + attn_fa_mx + attn_fd_combine (fa_mx.wgsl:19-115, 313-319;
+ * engine.rs:1215-1236) and attn_fa / attn_fd4 for the f32 store (ops.wgsl:540-651, 694-778). */
+int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, float scale, float* out,
+                const float* gate_src);
+
+/* Prefix-cache snapshot of positions [0, p) of every layer (the KV part of read_root / write_root,
+ * engine.rs:782-823). The byte image is the store's own layout, block-rounded; restore into a store of the same
+ * layers / format (any ctx >= p) gives back bit-identical positions [0, p) and sets every layer's length to p.
+ * host: pinned host memory (hipHostMalloc) of exactly mkv_snapshot_bytes(h, p) bytes.
+ * mkv_snapshot waits until the copy has landed in host memory; mkv_restore returns when the copy is enqueued
+ * (the host buffer must stay valid until mkv_sync). */
+size_t mkv_snapshot_bytes(const mkv_t* h, int p);
+int mkv_snapshot(mkv_t* h, int p, void* host, size_t bytes);
+int mkv_restore(mkv_t* h, int p, const void* host, size_t bytes);
+
+/* Conversion to / from the reference's position-major layout for positions [p0, p1) of one layer's K or V:
+ * dst/src (device) hold (p1 - p0) x 512 elements in the store's element type (f16 bit patterns or f32),
+ * element (pos, kvh, d) at (pos - p0)*512 + kvh*256 + d -- the words read_root writes for that range
+ * (engine.rs:784-802). mkv_write_rows extends the layer's length to p1 if p0 <= len. */
+int mkv_read_rows(mkv_t* h, int layer, int which, int p0, int p1, void* dst);
+int mkv_write_rows(mkv_t* h, int layer, int which, int p0, int p1, const void* src);
+
+/* rope_table(pos) on the host (engine.rs:108-114): tab[0..32) = cos, tab[32..64) = sin of th_i, th_0 = pos,
+ * th_{i+1} = th_i * 1e7^(-2/64), all in f32. */
+int mkv_rope_table(int pos, float* tab);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,214 @@
+"""mechta_amd: MI355X-native KV-cache path of mechta (f16/f32 KV store, append with rollback, split-K flash decode,
+causal prefill flash attention, prefix-cache snapshot), behind the C ABI of include/mechta_kv.h.
+
+This module is the Python host mirror of that ABI (ctypes over mechta_amd/lib/libmechta_kv.so). Device buffers are
+torch tensors used as plain HBM allocations; every compute call goes through the HIP library, and a missing or
+unloadable library raises instead of computing anything another way.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libmechta_kv.so")
+
+F16, F32 = 0, 1
+K, V = 0, 1
+KV_HEADS, Q_HEADS, HEAD_DIM = 2, 16, 256
+CTX_MIN, CTX_MAX = 4096, 262144
+PREFILL_MAX = 512
+
+E_ARG, E_CTX, E_POS, E_LAYER, E_SIZE, E_HIP, E_NOMEM, E_FMT = -1, -2, -3, -4, -5, -6, -7, -8
+
+# every symbol include/mechta_kv.h declares
+SYMBOLS = ["mkv_create", "mkv_destroy", "mkv_set_stream", "mkv_sync", "mkv_last_error", "mkv_info", "mkv_len",
+           "mkv_append", "mkv_set_len", "mkv_decode", "mkv_append_decode", "mkv_prefill", "mkv_snapshot_bytes",
+           "mkv_snapshot", "mkv_restore", "mkv_read_rows", "mkv_write_rows", "mkv_rope_table"]
+
+
+class MkvError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def lib():
+    """Loads libmechta_kv.so (raises if it was not built: run __graft_entry__.build())."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with python -c 'import __graft_entry__ as g; "
+                               f"g.build()'")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I, F, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+        sig = {
+            "mkv_create": ([ctypes.POINTER(P), I, I, I, P], I),
+            "mkv_destroy": ([P], I),
+            "mkv_set_stream": ([P, P], I),
+            "mkv_sync": ([P], I),
+            "mkv_last_error": ([], ctypes.c_char_p),
+            "mkv_info": ([P, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I)], I),
+            "mkv_len": ([P, I, ctypes.POINTER(I)], I),
+            "mkv_append": ([P, I, I, I, P, P, P], I),
+            "mkv_set_len": ([P, I], I),
+            "mkv_decode": ([P, I, P, I, I, I, F, P, P], I),
+            "mkv_append_decode": ([P, I, I, I, P, P, P, P, I, F, P, P], I),
+            "mkv_prefill": ([P, I, P, I, I, I, F, P, P], I),
+            "mkv_snapshot_bytes": ([P, I], S),
+            "mkv_snapshot": ([P, I, P, S], I),
+            "mkv_restore": ([P, I, P, S], I),
+            "mkv_read_rows": ([P, I, I, I, I, P], I),
+            "mkv_write_rows": ([P, I, I, I, I, P], I),
+            "mkv_rope_table": ([I, P], I),
+        }
+        for name, (args, res) in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise MkvError(rc, lib().mkv_last_error().decode())
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _dev(t, n, name):
+    """Checks a torch tensor argument: on a GPU, float32, contiguous, at least n elements."""
+    import torch
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous float32")
+    if t.numel() < n:
+        raise ValueError(f"{name} holds {t.numel()} values, {n} needed")
+    return _ptr(t)
+
+
+def rope_table(pos):
+    """rope_table(pos) of the reference (engine.rs:108-114), computed by the library's host code: 64 floats."""
+    buf = (ctypes.c_float * 64)()
+    _check(lib().mkv_rope_table(int(pos), buf))
+    return list(buf)
+
+
+class KvStore:
+    """The KV store of `layers` full-attention layers (K and V, 2 KV heads x 256, `ctx` positions, f16 or f32).
+
+    Mirrors the KV-cache part of the reference's Engine: append = kv_rope2 + kv_copy, decode = attn_fd / attn_dmx2 +
+    attn_fd_combine (+ attn_gate), prefill = attn_fa_mx + attn_fd_combine, snapshot/restore = read_root / write_root
+    (KV part). All tensors are torch device tensors; calls are ordered on `stream` (default: torch's current stream).
+    """
+
+    def __init__(self, layers, ctx, fmt=F16, stream=None):
+        import torch
+        self.layers, self.ctx, self.fmt = layers, ctx, fmt
+        s = stream if stream is not None else torch.cuda.current_stream()
+        self._stream = s
+        h = ctypes.c_void_p()
+        _check(lib().mkv_create(ctypes.byref(h), layers, ctx, fmt, ctypes.c_void_p(s.cuda_stream)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().mkv_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def set_stream(self, stream):
+        self._stream = stream
+        _check(lib().mkv_set_stream(self._h, ctypes.c_void_p(stream.cuda_stream)))
+
+    def sync(self):
+        _check(lib().mkv_sync(self._h))
+
+    def length(self, layer=0):
+        n = ctypes.c_int()
+        _check(lib().mkv_len(self._h, layer, ctypes.byref(n)))
+        return n.value
+
+    def append(self, layer, pos, k_normed, v, rope_tab):
+        ntok = k_normed.numel() // (KV_HEADS * HEAD_DIM)
+        _check(lib().mkv_append(self._h, layer, pos, ntok, _dev(k_normed, ntok * 512, "k_normed"),
+                                _dev(v, ntok * 512, "v"), _dev(rope_tab, ntok * 64, "rope_tab")))
+
+    def set_len(self, n):
+        _check(lib().mkv_set_len(self._h, n))
+
+    def decode(self, layer, q, n, start=0, scale=1.0 / 16, out=None, gate_src=None):
+        import torch
+        ntok = q.numel() // (Q_HEADS * HEAD_DIM)
+        if out is None:
+            out = torch.empty((ntok, Q_HEADS, HEAD_DIM), dtype=torch.float32, device=q.device)
+        g = None if gate_src is None else _dev(gate_src, ntok * Q_HEADS * 512, "gate_src")
+        _check(lib().mkv_decode(self._h, layer, _dev(q, ntok * 4096, "q"), ntok, n, start, scale,
+                                _dev(out, ntok * 4096, "out"), g))
+        return out
+
+    def append_decode(self, layer, n, k_normed, v, rope_tab, q, start=0, scale=1.0 / 16, out=None, gate_src=None):
+        import torch
+        ntok = q.numel() // (Q_HEADS * HEAD_DIM)
+        if out is None:
+            out = torch.empty((ntok, Q_HEADS, HEAD_DIM), dtype=torch.float32, device=q.device)
+        g = None if gate_src is None else _dev(gate_src, ntok * Q_HEADS * 512, "gate_src")
+        _check(lib().mkv_append_decode(self._h, layer, n, ntok, _dev(k_normed, ntok * 512, "k_normed"),
+                                       _dev(v, ntok * 512, "v"), _dev(rope_tab, ntok * 64, "rope_tab"),
+                                       _dev(q, ntok * 4096, "q"), start, scale, _dev(out, ntok * 4096, "out"), g))
+        return out
+
+    def prefill(self, layer, q, n, start=0, scale=1.0 / 16, out=None, gate_src=None):
+        import torch
+        T = q.numel() // (Q_HEADS * HEAD_DIM)
+        if out is None:
+            out = torch.empty((T, Q_HEADS, HEAD_DIM), dtype=torch.float32, device=q.device)
+        g = None if gate_src is None else _dev(gate_src, T * Q_HEADS * 512, "gate_src")
+        _check(lib().mkv_prefill(self._h, layer, _dev(q, T * 4096, "q"), T, n, start, scale,
+                                 _dev(out, T * 4096, "out"), g))
+        return out
+
+    def snapshot_bytes(self, p):
+        return lib().mkv_snapshot_bytes(self._h, p)
+
+    def snapshot(self, p, host=None):
+        """KV of positions [0, p) of every layer into pinned host memory (a uint8 tensor)."""
+        import torch
+        nb = self.snapshot_bytes(p)
+        if host is None:
+            host = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+        _check(lib().mkv_snapshot(self._h, p, _ptr(host), host.numel() * host.element_size()))
+        return host
+
+    def restore(self, p, host):
+        _check(lib().mkv_restore(self._h, p, _ptr(host), host.numel() * host.element_size()))
+
+    def read_rows(self, layer, which, p0, p1, out=None):
+        """Positions [p0, p1) of K or V in the reference layout [pos][2][256] (int16 bit patterns for f16)."""
+        import torch
+        dt = torch.int16 if self.fmt == F16 else torch.float32
+        if out is None:
+            out = torch.empty((p1 - p0, KV_HEADS, HEAD_DIM), dtype=dt, device="cuda")
+        _check(lib().mkv_read_rows(self._h, layer, which, p0, p1, _ptr(out)))
+        return out
+
+    def write_rows(self, layer, which, p0, p1, rows):
+        _check(lib().mkv_write_rows(self._h, layer, which, p0, p1, _ptr(rows)))

@@ -1,0 +1,53 @@
+"""Builds libmechta_kv.so (the HIP path and its C ABI) in-tree for gfx950 with hipcc.
+
+Every HIP source is compiled with -Xclang -target-feature -Xclang -packed-fp32-ops (no packed-FP32 instructions) and
+linked into mechta_amd/lib/libmechta_kv.so. The library has no dependency on torch or on oracle/.
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUTDIR = os.path.join(HERE, "lib")
+LIB = os.path.join(OUTDIR, "libmechta_kv.so")
+SOURCES = ["kv_store.cpp", "kv_append.hip", "kv_decode.hip", "kv_prefill.hip"]
+ARCH = os.environ.get("MKV_OFFLOAD_ARCH", "gfx950")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
+         "-packed-fp32-ops", "-Wall", "-Wno-unused-result", "-I", os.path.join(HERE, "..", "include")]
+
+
+def _compile(src, verbose):
+    obj = os.path.join(OUTDIR, "obj", os.path.splitext(src)[0] + ".o")
+    os.makedirs(os.path.dirname(obj), exist_ok=True)
+    lang = ["-x", "hip"]
+    cmd = [HIPCC] + FLAGS + lang + ["-c", os.path.join(CSRC, src), "-o", obj]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")
+    errs = [l for l in r.stderr.splitlines() if "warning" in l and "packed-fp32-ops" not in l]
+    if errs and verbose:
+        print("\n".join(errs))
+    return obj
+
+
+def build(verbose=False):
+    os.makedirs(OUTDIR, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

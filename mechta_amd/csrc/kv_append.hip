@@ -1,0 +1,160 @@
+// kv_append.hip -- K/V append (RoPE + f32->f16 RNE) and conversion to / from the reference's position-major layout.
+//
+// Append replaces the reference's writer kernels kv_rope / kv_rope2 / kv_copy (kv.wgsl:19-42) for the f16 cache and
+// rope / rope2 / copy (ops.wgsl:141-162, 275-286) for the f32 cache. One launch writes K and V of all ntok tokens:
+// work items [0, nk) are K items (token, kv head, 8 dims), the rest V items (V group of 8 positions, kv head, dim).
+#include "mkv_internal.h"
+
+namespace mkv {
+namespace {
+
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+__device__ inline unsigned short f2h(float x) {
+    _Float16 h = (_Float16)x;  // v_cvt_f16_f32: IEEE round to nearest even, subnormals kept
+    return __builtin_bit_cast(unsigned short, h);
+}
+
+// NEOX RoPE value of dim d of one 256-dim K row a (kv_src, kv.wgsl:19-23): d < 32: a[d]c[d] - a[d+32]s[d];
+// 32 <= d < 64 (i = d - 32): a[i]s[i] + a[d]c[i]; else a[d]. Products and sums rounded separately (no FMA).
+__device__ inline float rope_dim(const float* __restrict__ a, const float* __restrict__ tb, int d) {
+#pragma clang fp contract(off)
+    if (d < 32) {
+        float p1 = a[d] * tb[d];
+        float p2 = a[d + 32] * tb[32 + d];
+        return p1 - p2;
+    }
+    if (d < 64) {
+        int i = d - 32;
+        float p1 = a[i] * tb[32 + i];
+        float p2 = a[d] * tb[i];
+        return p1 + p2;
+    }
+    return a[d];
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(256) append_kernel(void* __restrict__ kplane0, void* __restrict__ kplane1,
+                                                     void* __restrict__ vplane0, void* __restrict__ vplane1, int pos,
+                                                     int ntok, const float* __restrict__ kn,
+                                                     const float* __restrict__ v, const float* __restrict__ tab,
+                                                     int nk, int ng) {
+    int id = blockIdx.x * blockDim.x + threadIdx.x;
+    if (id < nk) {
+        // K item: token t, kv head kh, dims d0..d0+7 (32 items per row)
+        int t = id / (KVH * 32), kh = (id / 32) % KVH, d0 = (id % 32) * 8;
+        const float* a = kn + ((size_t)t * KVH + kh) * HD;
+        const float* tb = tab + (size_t)t * 64;
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) r[j] = rope_dim(a, tb, d0 + j);
+        int p = pos + t;
+        if (FMT == 0) {
+            u16x8 w;
+#pragma unroll
+            for (int j = 0; j < 8; j++) w[j] = f2h(r[j]);
+            unsigned short* kp = (unsigned short*)(kh ? kplane1 : kplane0);
+            *(u16x8*)(kp + k_off(p, d0)) = w;
+        } else {
+            float* kp = (float*)(kh ? kplane1 : kplane0) + (size_t)p * HD + d0;
+            *(float4*)kp = make_float4(r[0], r[1], r[2], r[3]);
+            *(float4*)(kp + 4) = make_float4(r[4], r[5], r[6], r[7]);
+        }
+        return;
+    }
+    id -= nk;
+    if (FMT == 0) {
+        // V item: group g (relative to the first group touched), kv head kh, dim d
+        if (id >= ng * KVH * HD) return;
+        int gi = id / (KVH * HD), kh = (id / HD) % KVH, d = id % HD;
+        int g = pos / VGRP + gi;
+        int p0 = max(pos, g * VGRP), p1 = min(pos + ntok, g * VGRP + VGRP);
+        unsigned short* vp = (unsigned short*)(kh ? vplane1 : vplane0);
+        const float* src = v + (size_t)kh * HD + d;  // v[t][kh*256 + d], t = p - pos
+        if (p0 == g * VGRP && p1 == g * VGRP + VGRP) {
+            u16x8 w;
+#pragma unroll
+            for (int j = 0; j < 8; j++) w[j] = f2h(src[(size_t)(p0 + j - pos) * (KVH * HD)]);
+            *(u16x8*)(vp + v_off(p0, d)) = w;
+        } else {
+            for (int p = p0; p < p1; p++) vp[v_off(p, d)] = f2h(src[(size_t)(p - pos) * (KVH * HD)]);
+        }
+    } else {
+        // V item (f32): token t, kv head kh, 4 dims
+        if (id >= ntok * KVH * (HD / 4)) return;
+        int t = id / (KVH * HD / 4), kh = (id / (HD / 4)) % KVH, d0 = (id % (HD / 4)) * 4;
+        float4 x = *(const float4*)(v + (size_t)t * (KVH * HD) + kh * HD + d0);
+        *(float4*)((float*)(kh ? vplane1 : vplane0) + (size_t)(pos + t) * HD + d0) = x;
+    }
+}
+
+// Position-major <-> store layout for [p0, p1) of one (layer, K|V): element (pos, kvh, d) of the reference layout
+// at ((pos - p0)*2 + kvh)*256 + d.
+template <typename T, int DIR>  // DIR 0: store -> rows, 1: rows -> store
+__global__ void __launch_bounds__(256) rows_kernel(T* __restrict__ plane0, T* __restrict__ plane1,
+                                                   T* __restrict__ rows, int p0, int p1, int which, int fmt) {
+    size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t total = (size_t)(p1 - p0) * KVH * HD;
+    if (id >= total) return;
+    int d = id % HD, kh = (id / HD) % KVH, p = p0 + (int)(id / (KVH * HD));
+    T* plane = kh ? plane1 : plane0;
+    size_t o = fmt == 1 ? (size_t)p * HD + d : (which == 0 ? k_off(p, d) : v_off(p, d));
+    if (DIR == 0) rows[id] = plane[o];
+    else plane[o] = rows[id];
+}
+
+}  // namespace
+
+hipError_t launch_append(const Geom& g, void* base, int layer, int pos, int ntok, const float* kn, const float* v,
+                         const float* tab, hipStream_t s) {
+    char* b = (char*)base;
+    void* k0 = b + g.plane(layer, 0, 0) * g.plane_bytes();
+    void* k1 = b + g.plane(layer, 0, 1) * g.plane_bytes();
+    void* v0 = b + g.plane(layer, 1, 0) * g.plane_bytes();
+    void* v1 = b + g.plane(layer, 1, 1) * g.plane_bytes();
+    int nk = ntok * KVH * 32;
+    int ng = (pos + ntok - 1) / VGRP - pos / VGRP + 1;
+    int nv = g.fmt == 0 ? ng * KVH * HD : ntok * KVH * (HD / 4);
+    int blocks = (nk + nv + 255) / 256;
+    if (g.fmt == 0)
+        append_kernel<0><<<blocks, 256, 0, s>>>(k0, k1, v0, v1, pos, ntok, kn, v, tab, nk, ng);
+    else
+        append_kernel<1><<<blocks, 256, 0, s>>>(k0, k1, v0, v1, pos, ntok, kn, v, tab, nk, ng);
+    return hipGetLastError();
+}
+
+static hipError_t launch_rows(const Geom& g, const void* base, int layer, int which, int p0, int p1, void* rows,
+                              int dir, hipStream_t s) {
+    char* b = (char*)base;
+    void* q0 = b + g.plane(layer, which, 0) * g.plane_bytes();
+    void* q1 = b + g.plane(layer, which, 1) * g.plane_bytes();
+    size_t total = (size_t)(p1 - p0) * KVH * HD;
+    if (total == 0) return hipSuccess;
+    unsigned blocks = (unsigned)((total + 255) / 256);
+    if (g.fmt == 0) {
+        if (dir == 0)
+            rows_kernel<unsigned short, 0><<<blocks, 256, 0, s>>>((unsigned short*)q0, (unsigned short*)q1,
+                                                                  (unsigned short*)rows, p0, p1, which, 0);
+        else
+            rows_kernel<unsigned short, 1><<<blocks, 256, 0, s>>>((unsigned short*)q0, (unsigned short*)q1,
+                                                                  (unsigned short*)rows, p0, p1, which, 0);
+    } else {
+        if (dir == 0)
+            rows_kernel<float, 0><<<blocks, 256, 0, s>>>((float*)q0, (float*)q1, (float*)rows, p0, p1, which, 1);
+        else
+            rows_kernel<float, 1><<<blocks, 256, 0, s>>>((float*)q0, (float*)q1, (float*)rows, p0, p1, which, 1);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_read_rows(const Geom& g, const void* base, int layer, int which, int p0, int p1, void* dst,
+                            hipStream_t s) {
+    return launch_rows(g, base, layer, which, p0, p1, dst, 0, s);
+}
+
+hipError_t launch_write_rows(const Geom& g, void* base, int layer, int which, int p0, int p1, const void* src,
+                             hipStream_t s) {
+    return launch_rows(g, base, layer, which, p0, p1, const_cast<void*>(src), 1, s);
+}
+
+}  // namespace mkv

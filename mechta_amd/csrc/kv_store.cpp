@@ -1,0 +1,315 @@
+// kv_store.cpp -- the KV store object and the C ABI of libmechta_kv (declared in include/mechta_kv.h).
+//
+// The store replaces the reference's per-layer K/V wgpu buffers (engine.rs:493-496) and the host side of the
+// dispatches that touch them (uniform writes engine.rs:618-673, quad.rs:277-289, engine.rs:902-931; root I/O
+// engine.rs:782-823). Argument checks return the error codes of the header where the reference panics.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "../../include/mechta_kv.h"
+#include "mkv_internal.h"
+
+using namespace mkv;
+
+struct mkv_store {
+    Geom g;
+    void* base = nullptr;           // layers x {K, V} x 2 planes
+    hipStream_t stream = nullptr;
+    std::vector<int> len;           // written positions per layer
+    DecodeWs dws{nullptr, 0};
+    float* pws = nullptr;           // prefill partials
+    size_t pws_floats = 0;
+};
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(MKV_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int check_layer(const mkv_store* h, int layer) {
+    if (layer < 0 || layer >= h->g.layers) return fail(MKV_E_LAYER, "layer %d outside [0, %d)", layer, h->g.layers);
+    return MKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mkv_last_error(void) { return g_err; }
+
+int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
+    if (!out) return fail(MKV_E_ARG, "mkv_create: out is NULL");
+    *out = nullptr;
+    if (layers < 1 || layers > 4096) return fail(MKV_E_ARG, "mkv_create: layers %d", layers);
+    if (fmt != MKV_F16 && fmt != MKV_F32) return fail(MKV_E_ARG, "mkv_create: format %d (use MKV_F16 or MKV_F32)", fmt);
+    if (ctx % 1024 != 0 || ctx < MKV_CTX_MIN || ctx > MKV_CTX_MAX)
+        return fail(MKV_E_CTX, "context %d: must be a multiple of 1024 between %d and %d", ctx, MKV_CTX_MIN,
+                    MKV_CTX_MAX);
+    mkv_store* h = new (std::nothrow) mkv_store;
+    if (!h) return fail(MKV_E_NOMEM, "mkv_create: host allocation");
+    h->g.layers = layers;
+    h->g.ctx = ctx;
+    h->g.fmt = fmt;
+    h->g.plane_elems = (size_t)ctx * HD;
+    h->stream = (hipStream_t)stream;
+    h->len.assign(layers, 0);
+    size_t bytes = (size_t)layers * 2 * KVH * h->g.plane_bytes();
+    hipError_t e = hipMalloc(&h->base, bytes);
+    if (e != hipSuccess) {
+        delete h;
+        (void)hipGetLastError();
+        return fail(MKV_E_NOMEM, "mkv_create: hipMalloc of %zu bytes failed", bytes);
+    }
+    h->dws.max_chunks = ctx / 128 + 2;
+    size_t dws_bytes = (size_t)KVH * ROWS * h->dws.max_chunks * PART * sizeof(float);
+    h->pws_floats = prefill_ws_floats(ctx);
+    e = hipMalloc(&h->dws.part, dws_bytes);
+    if (e == hipSuccess && h->pws_floats) e = hipMalloc(&h->pws, h->pws_floats * sizeof(float));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(h->base);
+        if (h->dws.part) (void)hipFree(h->dws.part);
+        delete h;
+        return fail(MKV_E_NOMEM, "mkv_create: workspace allocation failed");
+    }
+    // zero fill: positions never written read as 0 (wgpu zero-initialises the reference's buffers)
+    e = hipMemsetAsync(h->base, 0, bytes, h->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+    if (e != hipSuccess) {
+        int rc = hip_fail(e, "mkv_create: zero fill");
+        (void)hipFree(h->base);
+        (void)hipFree(h->dws.part);
+        if (h->pws) (void)hipFree(h->pws);
+        delete h;
+        return rc;
+    }
+    *out = h;
+    return MKV_OK;
+}
+
+int mkv_destroy(mkv_t* h) {
+    if (!h) return MKV_OK;
+    hipError_t e = hipStreamSynchronize(h->stream);
+    (void)hipFree(h->base);
+    (void)hipFree(h->dws.part);
+    if (h->pws) (void)hipFree(h->pws);
+    delete h;
+    return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_destroy");
+}
+
+int mkv_set_stream(mkv_t* h, void* stream) {
+    if (!h) return fail(MKV_E_ARG, "mkv_set_stream: NULL handle");
+    h->stream = (hipStream_t)stream;
+    return MKV_OK;
+}
+
+int mkv_sync(mkv_t* h) {
+    if (!h) return fail(MKV_E_ARG, "mkv_sync: NULL handle");
+    hipError_t e = hipStreamSynchronize(h->stream);
+    return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_sync");
+}
+
+int mkv_info(const mkv_t* h, int* layers, int* ctx, int* fmt) {
+    if (!h) return fail(MKV_E_ARG, "mkv_info: NULL handle");
+    if (layers) *layers = h->g.layers;
+    if (ctx) *ctx = h->g.ctx;
+    if (fmt) *fmt = h->g.fmt;
+    return MKV_OK;
+}
+
+int mkv_len(const mkv_t* h, int layer, int* len) {
+    if (!h || !len) return fail(MKV_E_ARG, "mkv_len: NULL argument");
+    if (int rc = check_layer(h, layer)) return rc;
+    *len = h->len[layer];
+    return MKV_OK;
+}
+
+int mkv_append(mkv_t* h, int layer, int pos, int ntok, const float* kn, const float* v, const float* tab) {
+    if (!h || !kn || !v || !tab) return fail(MKV_E_ARG, "mkv_append: NULL argument");
+    if (int rc = check_layer(h, layer)) return rc;
+    if (ntok < 1 || ntok > MKV_PREFILL_MAX) return fail(MKV_E_ARG, "mkv_append: ntok %d outside [1, %d]", ntok,
+                                                        MKV_PREFILL_MAX);
+    if (pos < 0 || pos + ntok > h->g.ctx)
+        return fail(MKV_E_POS, "mkv_append: positions [%d, %d) outside the context %d", pos, pos + ntok, h->g.ctx);
+    if (pos > h->len[layer])
+        return fail(MKV_E_POS, "mkv_append: position %d leaves a hole after the written length %d", pos,
+                    h->len[layer]);
+    hipError_t e = launch_append(h->g, h->base, layer, pos, ntok, kn, v, tab, h->stream);
+    if (e != hipSuccess) return hip_fail(e, "mkv_append");
+    h->len[layer] = pos + ntok;
+    return MKV_OK;
+}
+
+int mkv_set_len(mkv_t* h, int len) {
+    if (!h) return fail(MKV_E_ARG, "mkv_set_len: NULL handle");
+    for (int l = 0; l < h->g.layers; l++)
+        if (len < 0 || len > h->len[l])
+            return fail(MKV_E_POS, "mkv_set_len: %d is past the written length %d of layer %d", len, h->len[l], l);
+    for (int l = 0; l < h->g.layers; l++) h->len[l] = len;
+    return MKV_OK;
+}
+
+static int check_attn(const mkv_t* h, const char* who, int layer, const float* q, int ntok, int maxtok, int n,
+                      int start, float* out) {
+    if (!h || !q || !out) return fail(MKV_E_ARG, "%s: NULL argument", who);
+    if (int rc = check_layer(h, layer)) return rc;
+    if (ntok < 1 || ntok > maxtok) return fail(MKV_E_ARG, "%s: %d tokens outside [1, %d]", who, ntok, maxtok);
+    if (n < 1 || start < 0 || start >= n) return fail(MKV_E_POS, "%s: n = %d, start = %d", who, n, start);
+    if (n + ntok - 1 > h->len[layer])
+        return fail(MKV_E_POS, "%s: reads positions up to %d, layer %d holds %d", who, n + ntok - 1, layer,
+                    h->len[layer]);
+    return MKV_OK;
+}
+
+int mkv_decode(mkv_t* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
+               const float* gate) {
+    if (int rc = check_attn(h, "mkv_decode", layer, q, ntok, 4, n, start, out)) return rc;
+    hipError_t e = launch_decode(h->g, h->base, layer, q, ntok, n, start, scale, out, gate, h->dws, h->stream);
+    return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_decode");
+}
+
+int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* kn, const float* v, const float* tab,
+                      const float* q, int start, float scale, float* out, const float* gate) {
+    if (ntok < 1 || ntok > 4) return fail(MKV_E_ARG, "mkv_append_decode: %d tokens outside [1, 4]", ntok);
+    if (int rc = mkv_append(h, layer, n - 1, ntok, kn, v, tab)) return rc;
+    return mkv_decode(h, layer, q, ntok, n, start, scale, out, gate);
+}
+
+int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, float scale, float* out,
+                const float* gate) {
+    if (int rc = check_attn(h, "mkv_prefill", layer, q, T, MKV_PREFILL_MAX, n, start, out)) return rc;
+    hipError_t e = launch_prefill(h->g, h->base, layer, q, T, n, start, scale, out, gate, h->pws, h->pws_floats,
+                                  h->stream);
+    if (e == hipErrorNotSupported) {
+        // no prefill kernel for this configuration: the decode kernel over groups of 4 tokens (same semantics)
+        for (int t0 = 0; t0 < T; t0 += 4) {
+            int nt = T - t0 < 4 ? T - t0 : 4;
+            e = launch_decode(h->g, h->base, layer, q + (size_t)t0 * QH * HD, nt, n + t0, start, scale,
+                              out + (size_t)t0 * QH * HD, gate ? gate + (size_t)t0 * QH * 512 : nullptr, h->dws,
+                              h->stream);
+            if (e != hipSuccess) break;
+        }
+    }
+    return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_prefill");
+}
+
+size_t mkv_snapshot_bytes(const mkv_t* h, int p) {
+    if (!h || p < 0 || p > h->g.ctx) return 0;
+    if (h->g.fmt == MKV_F32) return (size_t)h->g.layers * 2 * KVH * (size_t)p * HD * 4;
+    // f16: K planes in whole blocks of 32 positions, V planes in groups of 8 (the store's own layout)
+    size_t kb = (size_t)((p + KBLK - 1) / KBLK) * KBLK * HD * 2;
+    size_t vb = (size_t)((p + VGRP - 1) / VGRP) * VGRP * HD * 2;
+    return (size_t)h->g.layers * KVH * (kb + vb);
+}
+
+// Bytes of the [0, p) prefix of one plane of K (which = 0) or V (which = 1).
+static size_t prefix_bytes(const mkv_t* h, int which, int p) {
+    if (h->g.fmt == MKV_F32) return (size_t)p * HD * 4;
+    int unit = which == 0 ? KBLK : VGRP;
+    return (size_t)((p + unit - 1) / unit) * unit * HD * 2;
+}
+
+static int snap_copy(mkv_t* h, int p, void* host, const void* chost, size_t bytes, bool save) {
+    const char* who = save ? "mkv_snapshot" : "mkv_restore";
+    if (!h || (!host && !chost)) return fail(MKV_E_ARG, "%s: NULL argument", who);
+    if (p < 0 || p > h->g.ctx) return fail(MKV_E_POS, "%s: p = %d outside [0, %d]", who, p, h->g.ctx);
+    if (save)
+        for (int l = 0; l < h->g.layers; l++)
+            if (p > h->len[l]) return fail(MKV_E_POS, "%s: p = %d past the written length %d of layer %d", who, p,
+                                           h->len[l], l);
+    if (bytes != mkv_snapshot_bytes(h, p))
+        return fail(MKV_E_SIZE, "%s: %zu bytes given, %zu needed for %d positions", who, bytes,
+                    mkv_snapshot_bytes(h, p), p);
+    if (p == 0) {
+        if (!save) h->len.assign(h->g.layers, 0);
+        return MKV_OK;
+    }
+    // image order: for each layer, K planes (kvh 0, 1) then V planes (kvh 0, 1); each plane's prefix is one row of a
+    // 2D copy with the plane size as device pitch
+    const size_t kb = prefix_bytes(h, 0, p), vb = prefix_bytes(h, 1, p);
+    const size_t pb = h->g.plane_bytes();
+    char* dev = (char*)h->base;
+    char* hb = (char*)(save ? host : const_cast<void*>(chost));
+    hipError_t e = hipSuccess;
+    if (kb == vb) {
+        int rows = h->g.layers * 2 * KVH;
+        e = save ? hipMemcpy2DAsync(hb, kb, dev, pb, kb, rows, hipMemcpyDeviceToHost, h->stream)
+                 : hipMemcpy2DAsync(dev, pb, hb, kb, kb, rows, hipMemcpyHostToDevice, h->stream);
+    } else {
+        size_t off = 0;
+        for (int l = 0; l < h->g.layers && e == hipSuccess; l++) {
+            for (int which = 0; which < 2 && e == hipSuccess; which++) {
+                size_t w = which == 0 ? kb : vb;
+                char* d = dev + h->g.plane(l, which, 0) * pb;
+                e = save ? hipMemcpy2DAsync(hb + off, w, d, pb, w, KVH, hipMemcpyDeviceToHost, h->stream)
+                         : hipMemcpy2DAsync(d, pb, hb + off, w, w, KVH, hipMemcpyHostToDevice, h->stream);
+                off += w * KVH;
+            }
+        }
+    }
+    if (e == hipSuccess && save) e = hipStreamSynchronize(h->stream);
+    if (e != hipSuccess) return hip_fail(e, who);
+    if (!save) h->len.assign(h->g.layers, p);
+    return MKV_OK;
+}
+
+int mkv_snapshot(mkv_t* h, int p, void* host, size_t bytes) { return snap_copy(h, p, host, nullptr, bytes, true); }
+
+int mkv_restore(mkv_t* h, int p, const void* host, size_t bytes) {
+    return snap_copy(h, p, nullptr, host, bytes, false);
+}
+
+int mkv_read_rows(mkv_t* h, int layer, int which, int p0, int p1, void* dst) {
+    if (!h || !dst) return fail(MKV_E_ARG, "mkv_read_rows: NULL argument");
+    if (int rc = check_layer(h, layer)) return rc;
+    if (which != MKV_K && which != MKV_V) return fail(MKV_E_ARG, "mkv_read_rows: which = %d", which);
+    if (p0 < 0 || p1 < p0 || p1 > h->g.ctx) return fail(MKV_E_POS, "mkv_read_rows: [%d, %d)", p0, p1);
+    hipError_t e = launch_read_rows(h->g, h->base, layer, which, p0, p1, dst, h->stream);
+    return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_read_rows");
+}
+
+int mkv_write_rows(mkv_t* h, int layer, int which, int p0, int p1, const void* src) {
+    if (!h || !src) return fail(MKV_E_ARG, "mkv_write_rows: NULL argument");
+    if (int rc = check_layer(h, layer)) return rc;
+    if (which != MKV_K && which != MKV_V) return fail(MKV_E_ARG, "mkv_write_rows: which = %d", which);
+    if (p0 < 0 || p1 < p0 || p1 > h->g.ctx) return fail(MKV_E_POS, "mkv_write_rows: [%d, %d)", p0, p1);
+    if (p0 > h->len[layer])
+        return fail(MKV_E_POS, "mkv_write_rows: position %d leaves a hole after the written length %d", p0,
+                    h->len[layer]);
+    hipError_t e = launch_write_rows(h->g, h->base, layer, which, p0, p1, src, h->stream);
+    if (e != hipSuccess) return hip_fail(e, "mkv_write_rows");
+    if (p1 > h->len[layer]) h->len[layer] = p1;
+    return MKV_OK;
+}
+
+int mkv_rope_table(int pos, float* tab) {
+    if (!tab) return fail(MKV_E_ARG, "mkv_rope_table: NULL argument");
+    // engine.rs:108-114: f32 throughout; Rust's f32 powf / cos / sin are the platform libm's powf / cosf / sinf
+    float scale = powf(1e7f, -2.0f / 64.0f);
+    float th = (float)pos;
+    for (int i = 0; i < 32; i++) {
+        tab[i] = cosf(th);
+        tab[32 + i] = sinf(th);
+        th = th * scale;
+    }
+    return MKV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,144 @@
+"""ctypes wrapper of the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, as the checker of the HIP
+path. Caches handled here use the reference's position-major layout: [pos][kvh=2][256] per layer, f16 caches as
+uint16 bit patterns (see mkv_oracle.h).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libmkv_oracle.so")
+
+KVH, H, D = 2, 16, 256
+ROW = KVH * D
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            from oracle import build as _b  # noqa: WPS433 (build on first use, CPU only)
+            _b.build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        _lib.orc_f32_to_f16.argtypes = [F]
+        _lib.orc_f32_to_f16.restype = ctypes.c_uint16
+        _lib.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        _lib.orc_f16_to_f32.restype = F
+        _lib.orc_f32_to_f16_n.argtypes = [P, P, ctypes.c_int64]
+        _lib.orc_rope_table.argtypes = [ctypes.c_int32, P]
+        _lib.orc_append.argtypes = [I, P, P, I, I, P, P, P]
+        _lib.orc_attn_fd.argtypes = [I, P, P, P, I, I, I, F, I, P]
+        _lib.orc_attn_dmx.argtypes = [P, P, P, I, I, F, I, P]
+        _lib.orc_attn_fa_mx.argtypes = [P, P, P, I, I, I, F, I, P, I, P]
+        _lib.orc_attn_fa_f32.argtypes = [P, P, P, I, I, I, F, P, I, P]
+        _lib.orc_gate.argtypes = [P, P, I, P]
+        _lib.orc_threads.restype = I
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dt):
+    a = np.ascontiguousarray(a, dtype=dt)
+    return a
+
+
+def f32_to_f16_bits(x):
+    x = _c(x, np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_n(_p(x), _p(y), x.size)
+    return y
+
+
+def f16_bits_to_f32(h):
+    return np.ascontiguousarray(h, np.uint16).view(np.float16).astype(np.float32)
+
+
+def rope_table(pos):
+    t = np.empty(64, np.float32)
+    lib().orc_rope_table(int(pos), _p(t))
+    return t
+
+
+def rope_tables(pos, ntok):
+    return np.stack([rope_table(pos + t) for t in range(ntok)])
+
+
+def new_cache(ctx, fmt):
+    """One layer's K or V cache in the reference layout, zero filled (wgpu zero-initialises buffers)."""
+    return np.zeros((ctx, KVH, D), np.uint16 if fmt == 0 else np.float32)
+
+
+def append(fmt, kc, vc, pos, kn, v, tab):
+    kn = _c(kn, np.float32).reshape(-1, KVH, D)
+    ntok = kn.shape[0]
+    v = _c(v, np.float32).reshape(ntok, ROW)
+    tab = _c(tab, np.float32).reshape(ntok, 64)
+    assert kc.flags.c_contiguous and vc.flags.c_contiguous
+    assert pos + ntok <= kc.shape[0]
+    lib().orc_append(int(fmt), _p(kc), _p(vc), int(pos), ntok, _p(kn), _p(v), _p(tab))
+
+
+def attn_fd(fmt, kc, vc, q, n, start=0, scale=1.0 / 16, bb=128):
+    q = _c(q, np.float32).reshape(-1, H, D)
+    ntok = q.shape[0]
+    assert n + ntok - 1 <= kc.shape[0]
+    out = np.empty((ntok, H, D), np.float32)
+    lib().orc_attn_fd(int(fmt), _p(kc), _p(vc), _p(q), ntok, int(n), int(start), float(scale), int(bb), _p(out))
+    return out
+
+
+def attn_dmx(kc, vc, q, n, scale=1.0 / 16, ch=2048):
+    q = _c(q, np.float32).reshape(-1, H, D)
+    ntok = q.shape[0]
+    assert 1 <= ntok <= 4 and n + ntok - 1 <= kc.shape[0]
+    assert kc.dtype == np.uint16
+    out = np.empty((ntok, H, D), np.float32)
+    lib().orc_attn_dmx(_p(kc), _p(vc), _p(q), ntok, int(n), float(scale), int(ch), _p(out))
+    return out
+
+
+def attn_fa_mx(kc, vc, q, n, start=0, scale=1.0 / 16, ch=2048, sel=None):
+    q = _c(q, np.float32).reshape(-1, H, D)
+    T = q.shape[0]
+    assert kc.dtype == np.uint16 and n + T - 1 <= kc.shape[0]
+    if sel is None:
+        sel = np.arange(T, dtype=np.int32)
+    sel = _c(sel, np.int32)
+    out = np.empty((len(sel), H, D), np.float32)
+    lib().orc_attn_fa_mx(_p(kc), _p(vc), _p(q), T, int(n), int(start), float(scale), int(ch), _p(sel), len(sel),
+                         _p(out))
+    return out
+
+
+def attn_fa_f32(kc, vc, q, n, start=0, scale=1.0 / 16, sel=None):
+    q = _c(q, np.float32).reshape(-1, H, D)
+    T = q.shape[0]
+    assert kc.dtype == np.float32 and n + T - 1 <= kc.shape[0]
+    if sel is None:
+        sel = np.arange(T, dtype=np.int32)
+    sel = _c(sel, np.int32)
+    out = np.empty((len(sel), H, D), np.float32)
+    lib().orc_attn_fa_f32(_p(kc), _p(vc), _p(q), T, int(n), int(start), float(scale), _p(sel), len(sel), _p(out))
+    return out
+
+
+def gate(att, qf):
+    att = _c(att, np.float32).reshape(-1, H * D)
+    ntok = att.shape[0]
+    qf = _c(qf, np.float32).reshape(ntok, H * 512)
+    out = np.empty_like(att)
+    lib().orc_gate(_p(att), _p(qf), ntok, _p(out))
+    return out
+
+
+def threads():
+    return lib().orc_threads()

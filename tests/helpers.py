@@ -1,0 +1,62 @@
+"""Shared helpers of the tests: seeded inputs, tolerance checks, GPU <-> oracle plumbing."""
+import numpy as np
+
+from oracle import oracle as O
+
+H, KVH, D = 16, 2, 256
+
+# attention tolerance of the task (north star): max-abs 2e-3 and relative (Frobenius) 1e-3 against the oracle
+ATOL, RTOL = 2e-3, 1e-3
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def kv_inputs(seed, ntok):
+    """Seeded N(0,1) f32 inputs of an append of ntok tokens: k_normed [ntok][2][256], v [ntok][512]."""
+    r = rng(seed)
+    return (r.standard_normal((ntok, KVH, D), dtype=np.float32),
+            r.standard_normal((ntok, KVH * D), dtype=np.float32))
+
+
+def q_inputs(seed, ntok):
+    r = rng(seed)
+    return r.standard_normal((ntok, H, D), dtype=np.float32)
+
+
+def gate_inputs(seed, ntok):
+    r = rng(seed)
+    return r.standard_normal((ntok, H, 512), dtype=np.float32)
+
+
+def err_stats(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    max_abs = float(np.abs(got - ref).max())
+    rel = float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+    return max_abs, rel
+
+
+def assert_attn_close(got, ref, atol=ATOL, rtol=RTOL, what=""):
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    max_abs, rel = err_stats(got, ref)
+    assert max_abs <= atol and rel <= rtol, f"{what}: max-abs {max_abs:.3e} (tol {atol}), rel {rel:.3e} (tol {rtol})"
+    return max_abs, rel
+
+
+def exact_attention(kc, vc, q, n, start=0, scale=1.0 / 16):
+    """Textbook softmax attention in float64 (brute force), reference layout caches; token t sees [start, n + t)."""
+    K = O.f16_bits_to_f32(kc) if kc.dtype == np.uint16 else kc
+    V = O.f16_bits_to_f32(vc) if vc.dtype == np.uint16 else vc
+    K = K.astype(np.float64)
+    V = V.astype(np.float64)
+    q = np.asarray(q, np.float64).reshape(-1, H, D)
+    out = np.empty(q.shape)
+    for t in range(q.shape[0]):
+        e = n + t
+        for h in range(H):
+            s = K[start:e, h // 8] @ q[t, h] * scale
+            w = np.exp(s - s.max())
+            out[t, h] = (w @ V[start:e, h // 8]) / w.sum()
+    return out

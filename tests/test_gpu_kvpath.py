@@ -1,0 +1,269 @@
+"""GPU parity tests of the KV-cache path through the C ABI (libmechta_kv.so), against the CPU oracle.
+
+Bars: append bit-exact to the oracle (f32 -> f16 round to nearest even, RoPE without FMA); attention within
+max-abs 2e-3 and relative 1e-3 of the oracle restatement of the reference kernel for the same path (attn_fd for one
+f32-semantics token, attn_dmx for the f16 4-token verify, attn_fa_mx for the prefill); snapshot bit-identical.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import (assert_attn_close, exact_attention, gate_inputs, kv_inputs, q_inputs)
+
+pytestmark = pytest.mark.gpu
+
+F16, F32 = 0, 1
+
+
+@pytest.fixture(scope="module")
+def mk(torch_gpu):
+    import mechta_amd
+    mechta_amd.lib()
+    return mechta_amd
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def fill(torch, store, layer, fmt, n_pos, seed, chunks=(512,), oracle_caches=None):
+    """Appends n_pos seeded tokens to `layer` through the GPU path (in appends of the given sizes, cycled) and, if
+    oracle_caches is given, through the oracle too. Returns the inputs."""
+    kn, v = kv_inputs(seed, n_pos)
+    tab = O.rope_tables(0, n_pos)
+    pos, i = 0, 0
+    while pos < n_pos:
+        m = min(chunks[i % len(chunks)], n_pos - pos)
+        store.append(layer, pos, dev(torch, kn[pos:pos + m]), dev(torch, v[pos:pos + m]), dev(torch, tab[pos:pos + m]))
+        pos += m
+        i += 1
+    if oracle_caches is not None:
+        kc, vc = oracle_caches
+        O.append(fmt, kc, vc, 0, kn, v, tab)
+    return kn, v, tab
+
+
+def rows_np(store, layer, which, p0, p1):
+    t = store.read_rows(layer, which, p0, p1).cpu().numpy()
+    return t.view(np.uint16) if t.dtype == np.int16 else t
+
+
+def caches_np(store, layer, p1):
+    return rows_np(store, layer, 0, 0, p1), rows_np(store, layer, 1, 0, p1)
+
+
+# ------------------------------------------------------------------------------------------------ append ---------
+
+@pytest.mark.parametrize("fmt", [F16, F32])
+def test_append_bit_exact(torch_gpu, mk, fmt):
+    torch = torch_gpu
+    print(f"append fmt={fmt}", flush=True)
+    ctx, n_pos = 4096, 1000
+    kc, vc = O.new_cache(ctx, fmt), O.new_cache(ctx, fmt)
+    with mk.KvStore(2, ctx, fmt) as st:
+        # ragged appends: 1, 3, 4, 64, 7, 512 ... cross every block / group boundary of the store layout
+        fill(torch, st, 1, fmt, n_pos, seed=11, chunks=(1, 3, 4, 64, 7, 512, 2), oracle_caches=(kc, vc))
+        st.sync()
+        gk, gv = caches_np(st, 1, n_pos)
+        assert np.array_equal(gk, kc[:n_pos]), "K differs"
+        assert np.array_equal(gv, vc[:n_pos]), "V differs"
+        # layer 0 untouched
+        assert st.length(0) == 0 and st.length(1) == n_pos
+        assert not np.any(rows_np(st, 0, 0, 0, 64))
+
+
+def test_append_f16_special_values(torch_gpu, mk):
+    """Values at the f16 boundaries: overflow to inf, the largest finite, subnormals, ties, signed zero."""
+    torch = torch_gpu
+    specials = np.array([65504.0, 65519.99, 65520.0, 1e6, -1e6, 6.1035156e-05, 6.1e-05, 5.96e-08, 2.98e-08,
+                         2.99e-08, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, -0.0, 0.0, 1e-30, 3.14159265, -2.7182817],
+                        np.float32)
+    r = np.random.default_rng(5)
+    ntok = 8
+    kn = r.choice(specials, size=(ntok, 2, 256)).astype(np.float32)
+    v = r.choice(specials, size=(ntok, 512)).astype(np.float32)
+    tab = O.rope_tables(0, ntok)
+    kc, vc = O.new_cache(4096, F16), O.new_cache(4096, F16)
+    O.append(F16, kc, vc, 0, kn, v, tab)
+    with mk.KvStore(1, 4096, F16) as st:
+        st.append(0, 0, dev(torch, kn), dev(torch, v), dev(torch, tab))
+        gk, gv = caches_np(st, 0, ntok)
+    assert np.array_equal(gk, kc[:ntok]) and np.array_equal(gv, vc[:ntok])
+
+
+def test_append_rollback(torch_gpu, mk):
+    """Rejected drafts: append 4 at pos, keep 2 (set_len), append 4 at pos + 2: same cache as a clean sequence."""
+    torch = torch_gpu
+    ctx, n0 = 4096, 300
+    kn, v = kv_inputs(21, n0 + 8)
+    knb, vb = kv_inputs(22, 4)  # the rejected drafts' rows
+    tab = O.rope_tables(0, n0 + 8)
+    with mk.KvStore(1, ctx, F16) as a, mk.KvStore(1, ctx, F16) as b:
+        # a: the step at n0 wrote 4 rows, the sure token and 3 drafts; the first draft is accepted, the last two
+        # (rows n0 + 2, n0 + 3) are rejected
+        a.append(0, 0, dev(torch, kn[:n0 + 2]), dev(torch, v[:n0 + 2]), dev(torch, tab[:n0 + 2]))
+        a.append(0, n0 + 2, dev(torch, knb[:2]), dev(torch, vb[:2]), dev(torch, tab[n0 + 2:n0 + 4]))
+        b.append(0, 0, dev(torch, kn[:n0 + 2]), dev(torch, v[:n0 + 2]), dev(torch, tab[:n0 + 2]))
+        a.set_len(n0 + 2)
+        assert a.length() == n0 + 2
+        a.append(0, n0 + 2, dev(torch, kn[n0 + 2:n0 + 6]), dev(torch, v[n0 + 2:n0 + 6]), dev(torch, tab[n0 + 2:n0 + 6]))
+        b.append(0, n0 + 2, dev(torch, kn[n0 + 2:n0 + 6]), dev(torch, v[n0 + 2:n0 + 6]), dev(torch, tab[n0 + 2:n0 + 6]))
+        ka, va = caches_np(a, 0, n0 + 6)
+        kb, vb2 = caches_np(b, 0, n0 + 6)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb2)
+        q = dev(torch, q_inputs(23, 4))
+        oa = a.decode(0, q, n0 + 3).cpu().numpy()
+        ob = b.decode(0, q, n0 + 3).cpu().numpy()
+        assert np.array_equal(oa, ob)
+
+
+def test_errors(torch_gpu, mk):
+    torch = torch_gpu
+    with pytest.raises(mk.MkvError) as e:
+        mk.KvStore(1, 5000, F16)
+    assert e.value.code == mk.E_CTX
+    with mk.KvStore(2, 4096, F16) as st:
+        kn, v = kv_inputs(1, 4)
+        tab = O.rope_tables(0, 4)
+        args = (dev(torch, kn), dev(torch, v), dev(torch, tab))
+        with pytest.raises(mk.MkvError) as e:
+            st.append(0, 10, *args)  # hole
+        assert e.value.code == mk.E_POS
+        with pytest.raises(mk.MkvError) as e:
+            st.append(2, 0, *args)
+        assert e.value.code == mk.E_LAYER
+        st.append(0, 0, *args)
+        q = dev(torch, q_inputs(2, 4))
+        with pytest.raises(mk.MkvError) as e:
+            st.decode(0, q, 2)  # reads up to 5 > 4
+        assert e.value.code == mk.E_POS
+        with pytest.raises(mk.MkvError) as e:
+            st.set_len(5)
+        assert e.value.code == mk.E_POS
+        with pytest.raises(mk.MkvError) as e:
+            st.restore(4, torch.empty(3, dtype=torch.uint8))
+        assert e.value.code == mk.E_SIZE
+
+
+# ------------------------------------------------------------------------------------------------ decode ---------
+
+DECODE_CASES = [  # (ctx, n0 positions already in the cache, ntok, start)
+    (4096, 1, 1, 0), (4096, 31, 4, 0), (4096, 300, 4, 0), (4096, 1000, 1, 0), (4096, 4092, 4, 0),
+    (8192, 4096, 1, 0), (8192, 5000, 4, 0), (8192, 2047, 2, 0), (8192, 3000, 3, 1), (8192, 3000, 4, 700),
+]
+
+
+@pytest.mark.parametrize("ctx,n0,ntok,start", DECODE_CASES)
+def test_decode_f16(torch_gpu, mk, ctx, n0, ntok, start):
+    torch = torch_gpu
+    print(f"decode f16 ctx={ctx} n0={n0} ntok={ntok} start={start}", flush=True)
+    with mk.KvStore(1, ctx, F16) as st:
+        fill(torch, st, 0, F16, n0 + ntok - 1 if n0 + ntok - 1 > 0 else 1, seed=100 + n0)
+        q = q_inputs(200 + n0, ntok)
+        out = st.decode(0, dev(torch, q), n0, start=start).cpu().numpy()
+        kc, vc = caches_np(st, 0, n0 + ntok - 1)
+    ref = O.attn_dmx(kc, vc, q, n0) if start == 0 else O.attn_fd(F16, kc, vc, q, n0, start=start)
+    assert_attn_close(out, ref, what="vs oracle")
+    ex = exact_attention(kc, vc, q, n0, start=start)
+    assert_attn_close(out, ex, what="vs f64")
+    if ntok == 1:
+        assert_attn_close(out, O.attn_fd(F16, kc, vc, q, n0), what="vs attn_fd")
+
+
+@pytest.mark.parametrize("ctx,n0,ntok,start", [(4096, 300, 4, 0), (4096, 1000, 1, 0), (8192, 5000, 4, 17),
+                                               (4096, 2, 1, 0)])
+def test_decode_f32(torch_gpu, mk, ctx, n0, ntok, start):
+    torch = torch_gpu
+    print(f"decode f32 ctx={ctx} n0={n0} ntok={ntok}", flush=True)
+    with mk.KvStore(1, ctx, F32) as st:
+        fill(torch, st, 0, F32, n0 + ntok - 1, seed=300 + n0)
+        q = q_inputs(400 + n0, ntok)
+        out = st.decode(0, dev(torch, q), n0, start=start).cpu().numpy()
+        kc, vc = caches_np(st, 0, n0 + ntok - 1)
+    ref = O.attn_fd(F32, kc, vc, q, n0, start=start)
+    assert_attn_close(out, ref, atol=1e-5, rtol=1e-5, what="f32 vs attn_fd")
+
+
+def test_decode_gate(torch_gpu, mk):
+    torch = torch_gpu
+    n0, ntok = 777, 4
+    with mk.KvStore(1, 4096, F16) as st:
+        fill(torch, st, 0, F16, n0 + ntok - 1, seed=5)
+        q = q_inputs(6, ntok)
+        qf = gate_inputs(7, ntok)
+        out = st.decode(0, dev(torch, q), n0, gate_src=dev(torch, qf)).cpu().numpy()
+        kc, vc = caches_np(st, 0, n0 + ntok - 1)
+    ref = O.gate(O.attn_dmx(kc, vc, q, n0), qf).reshape(out.shape)
+    assert_attn_close(out, ref, what="gated")
+
+
+def test_append_decode_fused_entry(torch_gpu, mk):
+    torch = torch_gpu
+    n0 = 1234
+    kn, v = kv_inputs(31, 4)
+    tab = O.rope_tables(n0 - 1, 4)
+    q = q_inputs(32, 4)
+    with mk.KvStore(1, 4096, F16) as a, mk.KvStore(1, 4096, F16) as b:
+        fill(torch, a, 0, F16, n0 - 1, seed=33)
+        fill(torch, b, 0, F16, n0 - 1, seed=33)
+        oa = a.append_decode(0, n0, dev(torch, kn), dev(torch, v), dev(torch, tab), dev(torch, q)).cpu().numpy()
+        b.append(0, n0 - 1, dev(torch, kn), dev(torch, v), dev(torch, tab))
+        ob = b.decode(0, dev(torch, q), n0).cpu().numpy()
+    assert np.array_equal(oa, ob)
+
+
+# ------------------------------------------------------------------------------------------------ prefill --------
+
+@pytest.mark.parametrize("n0,T,start", [(2000, 64, 0), (100, 512, 0), (3000, 37, 0), (1, 16, 0), (2500, 96, 300)])
+def test_prefill_f16(torch_gpu, mk, n0, T, start):
+    torch = torch_gpu
+    print(f"prefill f16 n0={n0} T={T}", flush=True)
+    with mk.KvStore(1, 4096, F16) as st:
+        fill(torch, st, 0, F16, n0 + T - 1, seed=500 + T)
+        q = q_inputs(600 + T, T)
+        out = st.prefill(0, dev(torch, q), n0, start=start).cpu().numpy()
+        kc, vc = caches_np(st, 0, n0 + T - 1)
+    ref = O.attn_fa_mx(kc, vc, q, n0, start=start)
+    assert_attn_close(out, ref, what="prefill vs attn_fa_mx")
+
+
+def test_prefill_f32(torch_gpu, mk):
+    torch = torch_gpu
+    n0, T = 1500, 70
+    with mk.KvStore(1, 4096, F32) as st:
+        fill(torch, st, 0, F32, n0 + T - 1, seed=700)
+        q = q_inputs(701, T)
+        out = st.prefill(0, dev(torch, q), n0).cpu().numpy()
+        kc, vc = caches_np(st, 0, n0 + T - 1)
+    ref = O.attn_fa_f32(kc, vc, q, n0)
+    assert_attn_close(out, ref, atol=1e-5, rtol=1e-5, what="prefill f32")
+
+
+# ------------------------------------------------------------------------------------------------ snapshot -------
+
+@pytest.mark.parametrize("fmt,p", [(F16, 1000), (F16, 1024), (F32, 777), (F16, 1)])
+def test_snapshot_roundtrip(torch_gpu, mk, fmt, p):
+    torch = torch_gpu
+    print(f"snapshot fmt={fmt} p={p}", flush=True)
+    layers = 3
+    q = dev(torch, q_inputs(801, 4))
+    with mk.KvStore(layers, 4096, fmt) as a:
+        for l in range(layers):
+            fill(torch, a, l, fmt, p + 3, seed=810 + l)
+        a.set_len(p)
+        img = a.snapshot(p)
+        assert img.numel() == a.snapshot_bytes(p)
+        kn, v = kv_inputs(820, 4)
+        tab = O.rope_tables(p, 4)
+        outs_a = [a.append_decode(l, p + 1, dev(torch, kn), dev(torch, v), dev(torch, tab), q).cpu().numpy()
+                  for l in range(layers)]
+        rows_a = [caches_np(a, l, p) for l in range(layers)]
+    with mk.KvStore(layers, 8192, fmt) as b:  # a fresh store, another ctx
+        b.restore(p, img)
+        b.sync()
+        assert b.length(0) == p
+        for l in range(layers):
+            kb, vb = caches_np(b, l, p)
+            assert np.array_equal(kb, rows_a[l][0]) and np.array_equal(vb, rows_a[l][1])
+            ob = b.append_decode(l, p + 1, dev(torch, kn), dev(torch, v), dev(torch, tab), q).cpu().numpy()
+            assert np.array_equal(ob, outs_a[l]), f"layer {l}: outputs differ after restore"

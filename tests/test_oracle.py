@@ -1,0 +1,264 @@
+"""Pins the CPU oracle (oracle/mkv_oracle.c) against computations that do not share its formulas.
+
+Function -> what pins it:
+  orc_f32_to_f16     numpy's float16 cast (an independent IEEE round-to-nearest-even) on every f16 rounding boundary,
+                     the midpoints between neighbours (ties), overflow, subnormals and 2^20 random bit patterns;
+                     orc_f16_to_f32 on all 65536 patterns against numpy.
+  orc_rope_table     th_i = pos * r^i computed by an explicit f32 recurrence in numpy; cos/sin within 1 ulp of the
+                     float64 values of the same th_i (the libm routines are the reference's own choice of cosf/sinf).
+  orc_append         closed forms: pos 0 (cos 1, sin 0) copies K; dims >= 64 and V are the plain f16 rounding of the
+                     input; the pair (i, i+32) is rotated by th_i (norm kept, angle = th_i) within f32 rounding;
+                     rotating back by -th_i recovers the input; f32 format stores the unrounded values.
+  orc_attn_fd        float64 textbook softmax attention (brute force) within 1e-5; one key -> v; identical keys ->
+                     mean of V; block size (16, 128, 4096) does not change the result (merge invariance).
+  orc_attn_dmx       float64 brute force within the task tolerance; equal scores -> mean of the f16 V; lazy max
+                     threshold exercised by a large score jump (result still within tolerance).
+  orc_attn_fa_mx     float64 brute force; chunk size invariance (2048 vs 64); a selected subset of tokens equals the
+                     same rows of the full call.
+  orc_attn_fa_f32    float64 brute force within 1e-5.
+  orc_gate           sigmoid closed form at 0 (x/2), large positive (x), large negative (0).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import exact_attention, err_stats
+
+F16, F32 = 0, 1
+
+
+# ------------------------------------------------------------------------------------------------ f16 ------------
+
+def test_f16_from_f32_matches_numpy_on_boundaries():
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = allh.view(np.float16).astype(np.float32)
+    finite = np.isfinite(f)
+    vals = f[finite]
+    # midpoints between consecutive f16 values (ties) and values just beside them
+    srt = np.unique(vals.astype(np.float64))
+    mids = ((srt[:-1] + srt[1:]) / 2).astype(np.float32)
+    near = np.concatenate([np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf))])
+    extra = np.array([65504, 65519.996, 65520, 65536, 1e30, -1e30, np.inf, -np.inf, 2 ** -25, 2 ** -24, 1.5 * 2 ** -25,
+                      2 ** -26, 1e-45, -0.0, 0.0, 6.1035156e-05, 6.103515e-05], np.float32)
+    x = np.concatenate([vals, mids, near, extra]).astype(np.float32)
+    got = O.f32_to_f16_bits(x)
+    ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_f16_random_bits_and_nan():
+    r = np.random.default_rng(1)
+    bits = r.integers(0, 2 ** 32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    assert np.array_equal(O.f32_to_f16_bits(x), x.astype(np.float16).view(np.uint16))
+    nan = O.f32_to_f16_bits(np.array([np.nan], np.float32))[0]
+    assert (nan & 0x7c00) == 0x7c00 and (nan & 0x3ff) != 0
+
+
+def test_f16_to_f32_all_patterns():
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = allh.view(np.float16).astype(np.float32)
+    got = np.array([O.lib().orc_f16_to_f32(int(h)) for h in allh[::7]], np.float32)
+    r = ref[::7]
+    same = (got == r) | (np.isnan(got) & np.isnan(r))
+    assert same.all()
+
+
+# ------------------------------------------------------------------------------------------------ rope table -----
+
+@pytest.mark.parametrize("pos", [0, 1, 2, 17, 4096, 65535, 65536, 262143])
+def test_rope_table(pos):
+    t = O.rope_table(pos)
+    r = np.float32(1e7) ** np.float32(-2.0 / 64.0)
+    th = np.float32(pos)
+    for i in range(32):
+        c64, s64 = math.cos(float(th)), math.sin(float(th))
+        # within 1 ulp of the float64 value of the same f32 angle
+        assert abs(t[i] - c64) <= np.spacing(np.float32(abs(c64))) + 1e-45
+        assert abs(t[32 + i] - s64) <= np.spacing(np.float32(abs(s64))) + 1e-45
+        th = np.float32(th * r)
+    if pos == 0:
+        assert np.all(t[:32] == 1.0) and np.all(t[32:] == 0.0)
+
+
+# ------------------------------------------------------------------------------------------------ append ---------
+
+def test_append_pos0_is_plain_rounding():
+    r = np.random.default_rng(2)
+    kn = r.standard_normal((3, 2, 256), dtype=np.float32)
+    v = r.standard_normal((3, 512), dtype=np.float32)
+    kc, vc = O.new_cache(4096, F16), O.new_cache(4096, F16)
+    tab = np.tile(O.rope_table(0), (3, 1))  # angle 0 for all three tokens
+    O.append(F16, kc, vc, 5, kn, v, tab)
+    assert np.array_equal(kc[5:8], kn.astype(np.float16).view(np.uint16))
+    assert np.array_equal(vc[5:8].reshape(3, 512), v.astype(np.float16).view(np.uint16))
+    assert not kc[:5].any() and not kc[8:].any()
+
+
+def test_append_is_a_rotation():
+    r = np.random.default_rng(3)
+    pos, ntok = 1000, 4
+    kn = r.standard_normal((ntok, 2, 256), dtype=np.float32)
+    v = r.standard_normal((ntok, 512), dtype=np.float32)
+    tab = O.rope_tables(pos, ntok)
+    kc, vc = O.new_cache(4096, F32), O.new_cache(4096, F32)
+    O.append(F32, kc, vc, pos, kn, v, tab)
+    out = kc[pos:pos + ntok].astype(np.float64)
+    a = kn.astype(np.float64)
+    # dims >= 64 copied exactly, V copied exactly
+    assert np.array_equal(kc[pos:pos + ntok][:, :, 64:], kn[:, :, 64:])
+    assert np.array_equal(vc[pos:pos + ntok].reshape(ntok, 512), v)
+    rr = np.float32(1e7) ** np.float32(-2.0 / 64.0)
+    for t in range(ntok):
+        th = np.float32(pos + t)
+        for i in range(32):
+            x1, x2 = a[t, :, i], a[t, :, i + 32]
+            y1, y2 = out[t, :, i], out[t, :, i + 32]
+            # norm kept and angle = th_i, against float64 trigonometry of the f32 angle
+            c, s = math.cos(float(th)), math.sin(float(th))
+            assert np.allclose(y1, x1 * c - x2 * s, atol=1e-5)
+            assert np.allclose(y2, x1 * s + x2 * c, atol=1e-5)
+            assert np.allclose(np.hypot(y1, y2), np.hypot(x1, x2), rtol=1e-5)
+            th = np.float32(th * rr)
+    # rotating back by -th recovers the input
+    back = np.array(tab)
+    back[:, 32:] = -back[:, 32:]
+    kc2, vc2 = O.new_cache(4096, F32), O.new_cache(4096, F32)
+    O.append(F32, kc2, vc2, pos, kc[pos:pos + ntok], v, back)
+    assert np.allclose(kc2[pos:pos + ntok], kn, atol=1e-5)
+
+
+def test_append_f16_is_f32_then_rne():
+    r = np.random.default_rng(4)
+    kn = r.standard_normal((5, 2, 256), dtype=np.float32) * 100
+    v = r.standard_normal((5, 512), dtype=np.float32)
+    tab = O.rope_tables(777, 5)
+    k16, v16 = O.new_cache(4096, F16), O.new_cache(4096, F16)
+    k32, v32 = O.new_cache(4096, F32), O.new_cache(4096, F32)
+    O.append(F16, k16, v16, 10, kn, v, tab)
+    O.append(F32, k32, v32, 10, kn, v, tab)
+    assert np.array_equal(k16[10:15], k32[10:15].astype(np.float16).view(np.uint16))
+    assert np.array_equal(v16[10:15], v32[10:15].astype(np.float16).view(np.uint16))
+
+
+# ------------------------------------------------------------------------------------------------ attention ------
+
+def _cache(fmt, n, seed, ctx=4096):
+    r = np.random.default_rng(seed)
+    kn = r.standard_normal((n, 2, 256), dtype=np.float32)
+    v = r.standard_normal((n, 512), dtype=np.float32)
+    kc, vc = O.new_cache(ctx, fmt), O.new_cache(ctx, fmt)
+    O.append(fmt, kc, vc, 0, kn, v, O.rope_tables(0, n))
+    return kc, vc
+
+
+@pytest.mark.parametrize("fmt", [F16, F32])
+@pytest.mark.parametrize("n,ntok,start", [(1, 1, 0), (300, 4, 0), (1000, 1, 0), (777, 3, 100)])
+def test_attn_fd_vs_f64(fmt, n, ntok, start):
+    kc, vc = _cache(fmt, n + ntok - 1, 10 + n)
+    q = np.random.default_rng(n).standard_normal((ntok, 16, 256), dtype=np.float32)
+    got = O.attn_fd(fmt, kc, vc, q, n, start=start)
+    ex = exact_attention(kc, vc, q, n, start=start)
+    ma, rel = err_stats(got, ex)
+    assert ma < 1e-5 and rel < 1e-5
+
+
+def test_attn_fd_block_invariance():
+    kc, vc = _cache(F16, 1003, 20)
+    q = np.random.default_rng(21).standard_normal((4, 16, 256), dtype=np.float32)
+    a = O.attn_fd(F16, kc, vc, q, 1000, bb=16)
+    b = O.attn_fd(F16, kc, vc, q, 1000, bb=128)
+    c = O.attn_fd(F16, kc, vc, q, 1000, bb=4096)
+    assert np.allclose(a, b, atol=1e-6) and np.allclose(b, c, atol=1e-6)
+
+
+def test_attn_special_cases():
+    kc, vc = _cache(F16, 64, 30)
+    q = np.random.default_rng(31).standard_normal((1, 16, 256), dtype=np.float32)
+    v0 = O.f16_bits_to_f32(vc[0])
+    # one key: out = v of position 0, for every head
+    for fn in (lambda: O.attn_fd(F16, kc, vc, q, 1), lambda: O.attn_dmx(kc, vc, q, 1),
+               lambda: O.attn_fa_mx(kc, vc, q, 1)):
+        out = fn()
+        for h in range(16):
+            assert np.allclose(out[0, h], v0[h // 8], atol=1e-6)
+    # identical keys: uniform weights -> mean of V
+    kc2 = kc.copy()
+    kc2[:50] = kc2[0]
+    mean = O.f16_bits_to_f32(vc[:50]).astype(np.float64).mean(axis=0)
+    for fn in (lambda: O.attn_fd(F16, kc2, vc, q, 50), lambda: O.attn_dmx(kc2, vc, q, 50),
+               lambda: O.attn_fa_mx(kc2, vc, q, 50)):
+        out = fn()
+        for h in range(16):
+            assert np.allclose(out[0, h], mean[h // 8], atol=2e-3)
+    # uniform V: output = that V whatever the scores
+    vc3 = vc.copy()
+    vc3[:] = vc[7]
+    out = O.attn_dmx(kc, vc3, q, 60)
+    for h in range(16):
+        assert np.allclose(out[0, h], O.f16_bits_to_f32(vc[7])[h // 8], atol=1e-3)
+
+
+@pytest.mark.parametrize("n,ntok", [(1, 1), (100, 4), (2100, 4), (4093, 4), (3000, 2)])
+def test_attn_dmx_vs_f64(n, ntok):
+    kc, vc = _cache(F16, n + ntok - 1, 40 + n)
+    q = np.random.default_rng(41 + n).standard_normal((ntok, 16, 256), dtype=np.float32)
+    got = O.attn_dmx(kc, vc, q, n)
+    ex = exact_attention(kc, vc, q, n)
+    ma, rel = err_stats(got, ex)
+    assert ma < 2e-3 and rel < 1e-3
+    # f16 rounding of Q and P is really applied: not identical to the f32 path (one key: both give v exactly)
+    assert n == 1 or not np.array_equal(got, O.attn_fd(F16, kc, vc, q, n))
+
+
+def test_attn_dmx_lazy_max_jump():
+    """A late key with a score far above the early ones moves the lazy reference max (> 8 above it)."""
+    kc, vc = _cache(F16, 300, 50)
+    q = np.random.default_rng(51).standard_normal((4, 16, 256), dtype=np.float32)
+    # key 200 of kv head 0 parallel to q of head 0, token 0, with score q.k / 16 = 30
+    c = 30 * 16 / np.dot(q[0, 0], q[0, 0])
+    kc[200, 0] = (q[0, 0] * c).astype(np.float16).view(np.uint16)
+    got = O.attn_dmx(kc, vc, q, 297)
+    ex = exact_attention(kc, vc, q, 297)
+    ma, rel = err_stats(got, ex)
+    assert ma < 2e-3 and rel < 1e-3
+    assert np.allclose(got[0, 0], O.f16_bits_to_f32(vc[200, 0]), atol=1e-3)  # that key dominates head 0
+
+
+@pytest.mark.parametrize("n,T,start", [(2000, 64, 0), (10, 100, 0), (1500, 33, 200)])
+def test_attn_fa_mx_vs_f64(n, T, start):
+    kc, vc = _cache(F16, n + T - 1, 60 + T)
+    q = np.random.default_rng(61 + T).standard_normal((T, 16, 256), dtype=np.float32)
+    got = O.attn_fa_mx(kc, vc, q, n, start=start)
+    ex = exact_attention(kc, vc, q, n, start=start)
+    ma, rel = err_stats(got, ex)
+    assert ma < 2e-3 and rel < 1e-3
+    small = O.attn_fa_mx(kc, vc, q, n, start=start, ch=64)
+    assert np.allclose(small, got, atol=1e-5)
+    sel = np.array([0, T // 2, T - 1], np.int32)
+    part = O.attn_fa_mx(kc, vc, q, n, start=start, sel=sel)
+    assert np.array_equal(part, got[sel])
+
+
+def test_attn_fa_f32_vs_f64():
+    kc, vc = _cache(F32, 1000 + 40 - 1, 70)
+    q = np.random.default_rng(71).standard_normal((40, 16, 256), dtype=np.float32)
+    got = O.attn_fa_f32(kc, vc, q, 1000)
+    ex = exact_attention(kc, vc, q, 1000)
+    ma, rel = err_stats(got, ex)
+    assert ma < 1e-5 and rel < 1e-5
+
+
+def test_gate_closed_form():
+    att = np.random.default_rng(80).standard_normal((2, 16, 256), dtype=np.float32)
+    qf = np.zeros((2, 16, 512), np.float32)
+    assert np.allclose(O.gate(att, qf), att.reshape(2, -1) / 2)
+    qf[:, :, 256:] = 100.0
+    assert np.allclose(O.gate(att, qf), att.reshape(2, -1))
+    qf[:, :, 256:] = -100.0
+    assert np.allclose(O.gate(att, qf), 0.0, atol=1e-30)
+    qf[:, :, :256] = 1e9  # the q half of qf is not read
+    assert np.allclose(O.gate(att, qf), 0.0, atol=1e-30)
