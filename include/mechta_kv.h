@@ -133,6 +133,18 @@ int mkv_restore(mkv_t* h, int p, const void* host, size_t bytes);
 int mkv_read_rows(mkv_t* h, int layer, int which, int p0, int p1, void* dst);
 int mkv_write_rows(mkv_t* h, int layer, int which, int p0, int p1, const void* src);
 
+/* GPU time spans of the path's kernels: the counterpart of the reference's GPU timestamp spans around the attention
+ * groups attn.kv_write / attn.core / attn.merge (MECHTA_TRACE=2; gpu/src/lib.rs:297-341, engine.rs:1274-1299).
+ * While tracing is on, every kernel launch of the handle is bracketed by two HIP events on the handle's stream.
+ * mkv_trace(h, 1) starts (and clears), mkv_trace(h, 0) stops; mkv_trace_read waits for the stream and returns, per
+ * span, the summed kernel milliseconds and the number of launches since tracing started. */
+#define MKV_SPAN_KV_WRITE 0 /* append kernels */
+#define MKV_SPAN_CORE 1     /* split-K decode and prefill attention kernels */
+#define MKV_SPAN_MERGE 2    /* merge of the split-K partials (+ gate) */
+#define MKV_SPANS 3
+int mkv_trace(mkv_t* h, int enable);
+int mkv_trace_read(mkv_t* h, double* ms /*[MKV_SPANS]*/, long* count /*[MKV_SPANS]*/);
+
 /* rope_table(pos) on the host (engine.rs:108-114): tab[0..32) = cos, tab[32..64) = sin of th_i, th_0 = pos,
  * th_{i+1} = th_i * 1e7^(-2/64), all in f32. */
 int mkv_rope_table(int pos, float* tab);

@@ -22,7 +22,9 @@ E_ARG, E_CTX, E_POS, E_LAYER, E_SIZE, E_HIP, E_NOMEM, E_FMT = -1, -2, -3, -4, -5
 # every symbol include/mechta_kv.h declares
 SYMBOLS = ["mkv_create", "mkv_destroy", "mkv_set_stream", "mkv_sync", "mkv_last_error", "mkv_info", "mkv_len",
            "mkv_append", "mkv_set_len", "mkv_decode", "mkv_append_decode", "mkv_prefill", "mkv_snapshot_bytes",
-           "mkv_snapshot", "mkv_restore", "mkv_read_rows", "mkv_write_rows", "mkv_rope_table"]
+           "mkv_snapshot", "mkv_restore", "mkv_read_rows", "mkv_write_rows", "mkv_trace", "mkv_trace_read",
+           "mkv_rope_table"]
+SPAN_KV_WRITE, SPAN_CORE, SPAN_MERGE = 0, 1, 2
 
 
 class MkvError(RuntimeError):
@@ -61,6 +63,8 @@ def lib():
             "mkv_restore": ([P, I, P, S], I),
             "mkv_read_rows": ([P, I, I, I, I, P], I),
             "mkv_write_rows": ([P, I, I, I, I, P], I),
+            "mkv_trace": ([P, I], I),
+            "mkv_trace_read": ([P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_long)], I),
             "mkv_rope_table": ([I, P], I),
         }
         for name, (args, res) in sig.items():
@@ -185,6 +189,16 @@ class KvStore:
         _check(lib().mkv_prefill(self._h, layer, _dev(q, T * 4096, "q"), T, n, start, scale,
                                  _dev(out, T * 4096, "out"), g))
         return out
+
+    def trace(self, enable=True):
+        _check(lib().mkv_trace(self._h, 1 if enable else 0))
+
+    def trace_read(self):
+        """{span: (total kernel ms, launches)} for kv_write, core, merge since tracing started (waits)."""
+        ms = (ctypes.c_double * 3)()
+        cnt = (ctypes.c_long * 3)()
+        _check(lib().mkv_trace_read(self._h, ms, cnt))
+        return {name: (ms[i], cnt[i]) for i, name in enumerate(("kv_write", "core", "merge"))}
 
     def snapshot_bytes(self, p):
         return lib().mkv_snapshot_bytes(self._h, p)

@@ -318,33 +318,34 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
 
 }  // namespace
 
-int decode_chunk(int kend) {
-    int ch = (kend + 127) / 128;     // about 128 chunks per kv head: 256 work-groups for 256 CUs
-    ch = (ch + 31) / 32 * 32;        // whole 32-key tiles
-    return ch < 128 ? 128 : ch;
+DecodePlan decode_plan(int n, int ntok, int start) {
+    const int kend = n + ntok - 1;
+    int ch = (kend + 127) / 128;  // about 128 chunks per kv head: 256 work-groups for 256 CUs
+    ch = (ch + 31) / 32 * 32;     // whole 32-key tiles
+    if (ch < 128) ch = 128;
+    return DecodePlan{ch, (kend + ch - 1) / ch, start / ch};
 }
 
-hipError_t launch_decode(const Geom& g, const void* base, int layer, const float* q, int ntok, int n, int start,
-                         float scale, float* out, const float* gate, const DecodeWs& ws, hipStream_t s) {
-    const int kend = n + ntok - 1;
-    const int ch = decode_chunk(kend);
-    const int nch = (kend + ch - 1) / ch;
-    const int c0 = start / ch;
-    if (nch > ws.max_chunks) return hipErrorInvalidValue;
+hipError_t launch_decode_core(const Geom& g, const void* base, int layer, const float* q, int ntok, int n, int start,
+                              float scale, const DecodePlan& p, const DecodeWs& ws, hipStream_t s) {
+    if (p.nch > ws.max_chunks) return hipErrorInvalidValue;
     const char* b = (const char*)base;
     const void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
     const void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
     const float scale2 = scale * LOG2E;
-    dim3 grid(nch - c0, KVH);
+    dim3 grid(p.nch - p.c0, KVH);
     if (g.fmt == 0)
         decode_f16<<<grid, 256, 0, s>>>((const _Float16*)kp, (const _Float16*)vp, g.plane_elems, q, ntok, n, start,
-                                        scale2, ch, nch, c0, ws.part);
+                                        scale2, p.ch, p.nch, p.c0, ws.part);
     else
         decode_f32<<<grid, 256, 0, s>>>((const float*)kp, (const float*)vp, g.plane_elems, q, ntok, n, start, scale2,
-                                        ch, nch, c0, ws.part);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    decode_combine<<<ntok * QH, 256, 0, s>>>(ws.part, n, start, ch, nch, gate, out);
+                                        p.ch, p.nch, p.c0, ws.part);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
+                               float* out, hipStream_t s) {
+    decode_combine<<<ntok * QH, 256, 0, s>>>(ws.part, n, start, p.ch, p.nch, gate, out);
     return hipGetLastError();
 }
 

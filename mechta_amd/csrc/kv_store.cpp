@@ -25,6 +25,16 @@ struct mkv_store {
     DecodeWs dws{nullptr, 0};
     float* pws = nullptr;           // prefill partials
     size_t pws_floats = 0;
+    // tracing: events bracketing each kernel launch while on
+    bool tracing = false;
+    struct Span {
+        int kind;
+        hipEvent_t a, b;
+    };
+    std::vector<Span> pending;
+    std::vector<hipEvent_t> pool;
+    double ms[MKV_SPANS] = {0, 0, 0};
+    long count[MKV_SPANS] = {0, 0, 0};
 };
 
 namespace {
@@ -46,6 +56,51 @@ int hip_fail(hipError_t e, const char* what) {
 int check_layer(const mkv_store* h, int layer) {
     if (layer < 0 || layer >= h->g.layers) return fail(MKV_E_LAYER, "layer %d outside [0, %d)", layer, h->g.layers);
     return MKV_OK;
+}
+
+hipEvent_t take_event(mkv_store* h) {
+    if (!h->pool.empty()) {
+        hipEvent_t e = h->pool.back();
+        h->pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Runs `launch` (which enqueues one kernel on h->stream), bracketed by two events when tracing.
+template <typename F>
+hipError_t traced(mkv_store* h, int kind, F&& launch) {
+    if (!h->tracing) return launch();
+    hipEvent_t a = take_event(h), b = take_event(h);
+    if (!a || !b) return hipErrorOutOfMemory;
+    hipError_t e = hipEventRecord(a, h->stream);
+    if (e == hipSuccess) e = launch();
+    if (e == hipSuccess) e = hipEventRecord(b, h->stream);
+    if (e == hipSuccess) h->pending.push_back({kind, a, b});
+    return e;
+}
+
+hipError_t decode_all(mkv_store* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
+                      const float* gate) {
+    DecodePlan p = decode_plan(n, ntok, start);
+    hipError_t e = traced(h, MKV_SPAN_CORE, [&] {
+        return launch_decode_core(h->g, h->base, layer, q, ntok, n, start, scale, p, h->dws, h->stream);
+    });
+    if (e != hipSuccess) return e;
+    return traced(h, MKV_SPAN_MERGE,
+                  [&] { return launch_decode_merge(ntok, n, start, p, h->dws, gate, out, h->stream); });
+}
+
+void free_events(mkv_store* h) {
+    for (auto& s : h->pending) {
+        (void)hipEventDestroy(s.a);
+        (void)hipEventDestroy(s.b);
+    }
+    for (auto e : h->pool) (void)hipEventDestroy(e);
+    h->pending.clear();
+    h->pool.clear();
 }
 
 }  // namespace
@@ -107,6 +162,7 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
 int mkv_destroy(mkv_t* h) {
     if (!h) return MKV_OK;
     hipError_t e = hipStreamSynchronize(h->stream);
+    free_events(h);
     (void)hipFree(h->base);
     (void)hipFree(h->dws.part);
     if (h->pws) (void)hipFree(h->pws);
@@ -151,7 +207,8 @@ int mkv_append(mkv_t* h, int layer, int pos, int ntok, const float* kn, const fl
     if (pos > h->len[layer])
         return fail(MKV_E_POS, "mkv_append: position %d leaves a hole after the written length %d", pos,
                     h->len[layer]);
-    hipError_t e = launch_append(h->g, h->base, layer, pos, ntok, kn, v, tab, h->stream);
+    hipError_t e = traced(h, MKV_SPAN_KV_WRITE,
+                          [&] { return launch_append(h->g, h->base, layer, pos, ntok, kn, v, tab, h->stream); });
     if (e != hipSuccess) return hip_fail(e, "mkv_append");
     h->len[layer] = pos + ntok;
     return MKV_OK;
@@ -181,7 +238,7 @@ static int check_attn(const mkv_t* h, const char* who, int layer, const float* q
 int mkv_decode(mkv_t* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
                const float* gate) {
     if (int rc = check_attn(h, "mkv_decode", layer, q, ntok, 4, n, start, out)) return rc;
-    hipError_t e = launch_decode(h->g, h->base, layer, q, ntok, n, start, scale, out, gate, h->dws, h->stream);
+    hipError_t e = decode_all(h, layer, q, ntok, n, start, scale, out, gate);
     return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_decode");
 }
 
@@ -195,15 +252,16 @@ int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* kn, con
 int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, float scale, float* out,
                 const float* gate) {
     if (int rc = check_attn(h, "mkv_prefill", layer, q, T, MKV_PREFILL_MAX, n, start, out)) return rc;
-    hipError_t e = launch_prefill(h->g, h->base, layer, q, T, n, start, scale, out, gate, h->pws, h->pws_floats,
-                                  h->stream);
+    hipError_t e = traced(h, MKV_SPAN_CORE, [&] {
+        return launch_prefill(h->g, h->base, layer, q, T, n, start, scale, out, gate, h->pws, h->pws_floats,
+                              h->stream);
+    });
     if (e == hipErrorNotSupported) {
         // no prefill kernel for this configuration: the decode kernel over groups of 4 tokens (same semantics)
         for (int t0 = 0; t0 < T; t0 += 4) {
             int nt = T - t0 < 4 ? T - t0 : 4;
-            e = launch_decode(h->g, h->base, layer, q + (size_t)t0 * QH * HD, nt, n + t0, start, scale,
-                              out + (size_t)t0 * QH * HD, gate ? gate + (size_t)t0 * QH * 512 : nullptr, h->dws,
-                              h->stream);
+            e = decode_all(h, layer, q + (size_t)t0 * QH * HD, nt, n + t0, start, scale, out + (size_t)t0 * QH * HD,
+                           gate ? gate + (size_t)t0 * QH * 512 : nullptr);
             if (e != hipSuccess) break;
         }
     }
@@ -296,6 +354,46 @@ int mkv_write_rows(mkv_t* h, int layer, int which, int p0, int p1, const void* s
     hipError_t e = launch_write_rows(h->g, h->base, layer, which, p0, p1, src, h->stream);
     if (e != hipSuccess) return hip_fail(e, "mkv_write_rows");
     if (p1 > h->len[layer]) h->len[layer] = p1;
+    return MKV_OK;
+}
+
+int mkv_trace(mkv_t* h, int enable) {
+    if (!h) return fail(MKV_E_ARG, "mkv_trace: NULL handle");
+    if (enable) {
+        hipError_t e = hipStreamSynchronize(h->stream);
+        if (e != hipSuccess) return hip_fail(e, "mkv_trace");
+        for (auto& s : h->pending) {
+            h->pool.push_back(s.a);
+            h->pool.push_back(s.b);
+        }
+        h->pending.clear();
+        for (int i = 0; i < MKV_SPANS; i++) {
+            h->ms[i] = 0;
+            h->count[i] = 0;
+        }
+    }
+    h->tracing = enable != 0;
+    return MKV_OK;
+}
+
+int mkv_trace_read(mkv_t* h, double* ms, long* count) {
+    if (!h || !ms || !count) return fail(MKV_E_ARG, "mkv_trace_read: NULL argument");
+    hipError_t e = hipStreamSynchronize(h->stream);
+    if (e != hipSuccess) return hip_fail(e, "mkv_trace_read");
+    for (auto& s : h->pending) {
+        float t = 0.f;
+        e = hipEventElapsedTime(&t, s.a, s.b);
+        if (e != hipSuccess) return hip_fail(e, "mkv_trace_read: elapsed time");
+        h->ms[s.kind] += t;
+        h->count[s.kind] += 1;
+        h->pool.push_back(s.a);
+        h->pool.push_back(s.b);
+    }
+    h->pending.clear();
+    for (int i = 0; i < MKV_SPANS; i++) {
+        ms[i] = h->ms[i];
+        count[i] = h->count[i];
+    }
     return MKV_OK;
 }
 

@@ -49,10 +49,15 @@ hipError_t launch_read_rows(const Geom& g, const void* base, int layer, int whic
                             hipStream_t s);
 hipError_t launch_write_rows(const Geom& g, void* base, int layer, int which, int p0, int p1, const void* src,
                              hipStream_t s);
-// Chunk size (positions per work-group) the decode uses for a key range ending at kend.
-int decode_chunk(int kend);
-hipError_t launch_decode(const Geom& g, const void* base, int layer, const float* q, int ntok, int n, int start,
-                         float scale, float* out, const float* gate, const DecodeWs& ws, hipStream_t s);
+// Split-K pass and merge of the decode (two kernels, both on stream s).
+struct DecodePlan {
+    int ch, nch, c0;
+};
+DecodePlan decode_plan(int n, int ntok, int start);
+hipError_t launch_decode_core(const Geom& g, const void* base, int layer, const float* q, int ntok, int n, int start,
+                              float scale, const DecodePlan& p, const DecodeWs& ws, hipStream_t s);
+hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
+                               float* out, hipStream_t s);
 hipError_t launch_prefill(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
                           float scale, float* out, const float* gate, float* ws, size_t ws_floats, hipStream_t s);
 size_t prefill_ws_floats(int ctx);
