@@ -10,29 +10,6 @@ namespace {
 
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
-__device__ inline unsigned short f2h(float x) {
-    _Float16 h = (_Float16)x;  // v_cvt_f16_f32: IEEE round to nearest even, subnormals kept
-    return __builtin_bit_cast(unsigned short, h);
-}
-
-// NEOX RoPE value of dim d of one 256-dim K row a (kv_src, kv.wgsl:19-23): d < 32: a[d]c[d] - a[d+32]s[d];
-// 32 <= d < 64 (i = d - 32): a[i]s[i] + a[d]c[i]; else a[d]. Products and sums rounded separately (no FMA).
-__device__ inline float rope_dim(const float* __restrict__ a, const float* __restrict__ tb, int d) {
-#pragma clang fp contract(off)
-    if (d < 32) {
-        float p1 = a[d] * tb[d];
-        float p2 = a[d + 32] * tb[32 + d];
-        return p1 - p2;
-    }
-    if (d < 64) {
-        int i = d - 32;
-        float p1 = a[i] * tb[32 + i];
-        float p2 = a[d] * tb[i];
-        return p1 + p2;
-    }
-    return a[d];
-}
-
 template <int FMT>
 __global__ void __launch_bounds__(256) append_kernel(void* __restrict__ kplane0, void* __restrict__ kplane1,
                                                      void* __restrict__ vplane0, void* __restrict__ vplane1, int pos,
@@ -106,7 +83,7 @@ __global__ void __launch_bounds__(256) rows_kernel(T* __restrict__ plane0, T* __
 }  // namespace
 
 hipError_t launch_append(const Geom& g, void* base, int layer, int pos, int ntok, const float* kn, const float* v,
-                         const float* tab, hipStream_t s) {
+                         const float* tab, const Launch& L) {
     char* b = (char*)base;
     void* k0 = b + g.plane(layer, 0, 0) * g.plane_bytes();
     void* k1 = b + g.plane(layer, 0, 1) * g.plane_bytes();
@@ -116,45 +93,33 @@ hipError_t launch_append(const Geom& g, void* base, int layer, int pos, int ntok
     int ng = (pos + ntok - 1) / VGRP - pos / VGRP + 1;
     int nv = g.fmt == 0 ? ng * KVH * HD : ntok * KVH * (HD / 4);
     int blocks = (nk + nv + 255) / 256;
-    if (g.fmt == 0)
-        append_kernel<0><<<blocks, 256, 0, s>>>(k0, k1, v0, v1, pos, ntok, kn, v, tab, nk, ng);
-    else
-        append_kernel<1><<<blocks, 256, 0, s>>>(k0, k1, v0, v1, pos, ntok, kn, v, tab, nk, ng);
-    return hipGetLastError();
+    return launch(g.fmt == 0 ? append_kernel<0> : append_kernel<1>, dim3(blocks), dim3(256), L, k0, k1, v0, v1, pos,
+                  ntok, kn, v, tab, nk, ng);
 }
 
 static hipError_t launch_rows(const Geom& g, const void* base, int layer, int which, int p0, int p1, void* rows,
-                              int dir, hipStream_t s) {
+                              int dir, const Launch& L) {
     char* b = (char*)base;
     void* q0 = b + g.plane(layer, which, 0) * g.plane_bytes();
     void* q1 = b + g.plane(layer, which, 1) * g.plane_bytes();
     size_t total = (size_t)(p1 - p0) * KVH * HD;
     if (total == 0) return hipSuccess;
     unsigned blocks = (unsigned)((total + 255) / 256);
-    if (g.fmt == 0) {
-        if (dir == 0)
-            rows_kernel<unsigned short, 0><<<blocks, 256, 0, s>>>((unsigned short*)q0, (unsigned short*)q1,
-                                                                  (unsigned short*)rows, p0, p1, which, 0);
-        else
-            rows_kernel<unsigned short, 1><<<blocks, 256, 0, s>>>((unsigned short*)q0, (unsigned short*)q1,
-                                                                  (unsigned short*)rows, p0, p1, which, 0);
-    } else {
-        if (dir == 0)
-            rows_kernel<float, 0><<<blocks, 256, 0, s>>>((float*)q0, (float*)q1, (float*)rows, p0, p1, which, 1);
-        else
-            rows_kernel<float, 1><<<blocks, 256, 0, s>>>((float*)q0, (float*)q1, (float*)rows, p0, p1, which, 1);
-    }
-    return hipGetLastError();
+    if (g.fmt == 0)
+        return launch(dir == 0 ? rows_kernel<unsigned short, 0> : rows_kernel<unsigned short, 1>, dim3(blocks),
+                      dim3(256), L, q0, q1, rows, p0, p1, which, 0);
+    return launch(dir == 0 ? rows_kernel<float, 0> : rows_kernel<float, 1>, dim3(blocks), dim3(256), L, q0, q1, rows,
+                  p0, p1, which, 1);
 }
 
 hipError_t launch_read_rows(const Geom& g, const void* base, int layer, int which, int p0, int p1, void* dst,
-                            hipStream_t s) {
-    return launch_rows(g, base, layer, which, p0, p1, dst, 0, s);
+                            const Launch& L) {
+    return launch_rows(g, base, layer, which, p0, p1, dst, 0, L);
 }
 
 hipError_t launch_write_rows(const Geom& g, void* base, int layer, int which, int p0, int p1, const void* src,
-                             hipStream_t s) {
-    return launch_rows(g, base, layer, which, p0, p1, const_cast<void*>(src), 1, s);
+                             const Launch& L) {
+    return launch_rows(g, base, layer, which, p0, p1, const_cast<void*>(src), 1, L);
 }
 
 }  // namespace mkv

@@ -18,6 +18,8 @@
 // decode_combine: one work-group per (token, head), thread = dim: o = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c
 // over the chunks holding a visible key, then the optional sigmoid output gate (attn_gate, ops.wgsl:171-177).
 // Partials keep m in log2 units (scores are pre-multiplied by scale * log2 e).
+#include <type_traits>
+
 #include "mkv_internal.h"
 
 namespace mkv {
@@ -25,170 +27,222 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LAZY2 = 8.0f * LOG2E;  // DM_LAZY = 8 (dmx.rs:124) in log2 units
 constexpr float NEG_INF = -__builtin_huge_valf();
+constexpr int KPS = 64;                        // keys per stage of the decode ring
+constexpr int PS_STRIDE = KPS + 8;             // halves per P row in LDS (conflict-free 16-byte reads)
+constexpr int MERGE_J = 9;  // chunks per merge lane: 16 lanes x 9 >= the at most 130 chunks of decode_plan
 
 __device__ inline f32x16 mfma32(half8 a, half8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Key offset inside a 32-key tile of the K row loaded by A-operand row m. The C layout of the 32x32 MFMA gives lane
-// half h the rows 8a + 4h + b (register 4a + b); loading row m from key perm(m) makes register i of lane half h hold
-// key 8h + i (i < 8) or 16 + 8h + (i - 8) (i >= 8): exactly the keys the P operand of the PV MFMA needs in that lane.
-__device__ inline int key_perm(int m) {
-    int a = m >> 3, c = (m >> 2) & 1, b = m & 3;
-    return 16 * (a >> 1) + 8 * c + 4 * (a & 1) + b;
+__device__ inline f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__global__ void __launch_bounds__(256) decode_f16(const _Float16* __restrict__ kplane, const _Float16* __restrict__ vplane,
+// Reduction over the 16 lanes of a DPP row (a row of S): quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror -- lane swaps inside the ALU, no LDS round trip.
+template <typename Op>
+__device__ inline float reduce16(float x, Op op) {
+    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true)));
+    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true)));
+    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true)));
+    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true)));
+    return x;
+}
+
+// Work-group barrier for LDS traffic only: waits for this wave's LDS operations, not for its global loads (a
+// __syncthreads() would also wait for every pending global load and drain the prefetched stages).
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One stage of this wave's registers: K operands (16 keys x 128 dims) and V operands (64 keys x 32 dims).
+struct StageRegs {
+    half8 k[4];
+    half8 v[4];
+};
+
+__global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane, _Float16* __restrict__ vplane,
                                                   size_t plane_elems, const float* __restrict__ q, int ntok, int n,
                                                   int start, float scale2, int ch, int nch, int c0,
-                                                  float* __restrict__ part) {
-    const int kvh = blockIdx.y, c = c0 + blockIdx.x;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int h = lane >> 5, r = lane & 31;
+                                                  float* __restrict__ part, const float* __restrict__ akn,
+                                                  const float* __restrict__ av, const float* __restrict__ atab,
+                                                  int apos, int antok) {
+    const int kvh = blockIdx.y, c = c0 + blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int h = lane >> 5, r = lane & 31, l16 = lane & 15, g4 = lane >> 4;
     const int kend = n + ntok - 1;
     const int cs = c * ch, ce = min(cs + ch, kend);
-    const _Float16* K = kplane + (size_t)kvh * plane_elems;
-    const _Float16* V = vplane + (size_t)kvh * plane_elems;
+    _Float16* K = kplane + (size_t)kvh * plane_elems;
+    _Float16* V = vplane + (size_t)kvh * plane_elems;
 
-    // Q as the B operand: lane (r, h) holds row r, dims 16s + 8h + 0..7 for step s, rounded to f16 (q_dmx).
-    const int t = r >> 3;
-    const int vis = n + t;  // row r sees keys < vis
-    half8 qb[16];
+    __shared__ float ss[2][ROWS][KPS + 1];  // partial S of the two dim halves, [row][key]
+    __shared__ __attribute__((aligned(16))) _Float16 ps[ROWS][PS_STRIDE];
+    __shared__ __attribute__((aligned(16))) float cfs[ROWS];
+
+    // Fused append (mkv_append_decode): the work-group whose chunk holds new rows writes this kv head's K and V of
+    // those rows (the same arithmetic as append_kernel) and makes them visible before any stage is loaded.
     {
-        const float* qrow = q + ((size_t)t * QH + kvh * GQA + (r & 7)) * HD + 8 * h;
+        const int p0 = max(apos, cs), p1 = min(apos + antok, cs + ch);
+        if (p0 < p1) {
+            unsigned short* Ku = (unsigned short*)K;
+            unsigned short* Vu = (unsigned short*)V;
+            for (int it = tid; it < (p1 - p0) * 32; it += 512) {
+                const int p = p0 + (it >> 5), d0 = (it & 31) * 8, t = p - apos;
+                const float* a = akn + ((size_t)t * KVH + kvh) * HD;
+                const float* tb = atab + (size_t)t * 64;
+                u16x8 w8;
 #pragma unroll
-        for (int s = 0; s < 16; s++) {
-            float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-            if (t < ntok) {
-                x0 = *(const float4*)(qrow + 16 * s);
-                x1 = *(const float4*)(qrow + 16 * s + 4);
+                for (int j = 0; j < 8; j++) w8[j] = f2h(rope_dim(a, tb, d0 + j));
+                *(u16x8*)(Ku + k_off(p, d0)) = w8;
             }
-            qb[s] = half8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
-                          (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
+            for (int it = tid; it < (p1 - p0) * HD; it += 512) {
+                const int p = p0 + it / HD, d = it % HD;
+                Vu[v_off(p, d)] = f2h(av[(size_t)(p - apos) * (KVH * HD) + kvh * HD + d]);
+            }
+            __threadfence();
+            __syncthreads();
         }
     }
-    float m = NEG_INF, lsum = 0.f;
-    f32x16 O[8];
-#pragma unroll
-    for (int nb = 0; nb < 8; nb++) O[nb] = f32x16{};
 
-    const int pk = key_perm(r);
-    const int ntiles = (ce - cs + 31) / 32;
-    for (int ti = w; ti < ntiles; ti += 4) {
-        const int k0 = cs + ti * 32;
-        // K tile: A operand of step s = 16 bytes of key k0 + pk, dims 16s + 8h .. +7
-        const _Float16* kb = K + (size_t)(k0 / KBLK) * (KBLK * HD) + h * (KBLK * 8) + pk * 8;
-        half8 ka[16];
+    // Roles of wave w in a 64-key stage:
+    //   S: keys 16kq .. 16kq + 15 (kq = w % 4) times dims 128dh .. 128dh + 127 (dh = w / 4), both 16-row halves,
+    //      v_mfma_f32_16x16x32_f16 with A = K (lane: key 16kq + lane%16, 8 dims at 32s + 8(lane/16)), B = Q^T;
+    //      the two dim halves' partial S meet in LDS;
+    //   P.V: dims 32w .. 32w + 31 of all 32 rows, v_mfma_f32_32x32x16_f16, B = V (lane: dim 32w + lane%32,
+    //      8 keys 16s2 + 8(lane/32) .. of group 2s2 + lane/32).
+    const int kq = w & 3, dh = w >> 2;
+    const int nst = (ce - cs + KPS - 1) / KPS;
+    const int kkey = 16 * kq + l16;  // S-role key inside the stage
+    auto load = [&](int j, StageRegs& R) {
+        const int k0 = cs + j * KPS;
+        const _Float16* kb = K + (size_t)((k0 + kkey) / KBLK) * (KBLK * HD) + ((k0 + kkey) % KBLK) * 8;
 #pragma unroll
-        for (int s = 0; s < 16; s++) ka[s] = *(const half8*)(kb + s * 2 * (KBLK * 8));
-        // V tile: B operand (dims 32nb + r, keys 16s2 + 8h .. +7) = 16 bytes of group k0/8 + 2s2 + h at dim
-        const _Float16* vb = V + (size_t)(k0 / VGRP + h) * (VGRP * HD) + r * VGRP;
-        half8 va[2][8];
+        for (int s = 0; s < 4; s++) R.k[s] = *(const half8*)(kb + (16 * dh + 4 * s + g4) * (KBLK * 8));
+        const _Float16* vb = V + (size_t)(k0 / VGRP + h) * (VGRP * HD) + (32 * w + r) * VGRP;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-            for (int nb = 0; nb < 8; nb++) va[s2][nb] = *(const half8*)(vb + s2 * 2 * (VGRP * HD) + nb * 32 * VGRP);
+        for (int s2 = 0; s2 < 4; s2++) R.v[s2] = *(const half8*)(vb + s2 * 2 * (VGRP * HD));
+    };
+    StageRegs RA, RB, RC;
+    if (nst > 0) load(0, RA);
+    if (nst > 1) load(1, RB);
 
-        f32x16 S = f32x16{};
+    // Q (rounded to f16 as q_dmx) as B operand, straight into registers: rows 16hb + lane%16, dims
+    // 128dh + 32s + 8(lane/16) .. +7; rows of absent tokens are zero
+    half8 qb[2][4];
 #pragma unroll
-        for (int s = 0; s < 16; s++) S = mfma32(ka[s], qb[s], S);
-
-        float mt = NEG_INF;
+    for (int hb = 0; hb < 2; hb++) {
+        const int row = 16 * hb + l16, tq = row >> 3;
+        const float* qr = q + ((size_t)min(tq, ntok - 1) * QH + kvh * GQA + (row & 7)) * HD + 128 * dh + 8 * g4;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            int key = k0 + 8 * h + i + (i >= 8 ? 8 : 0);
-            float sv = S[i] * scale2;
-            sv = (key < vis && key >= start) ? sv : NEG_INF;
-            S[i] = sv;
-            mt = fmaxf(mt, sv);
+        for (int s = 0; s < 4; s++) {
+            float4 x0 = *(const float4*)(qr + 32 * s), x1 = *(const float4*)(qr + 32 * s + 4);
+            if (tq >= ntok) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+            qb[hb][s] = half8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
+                              (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        float mr = m;
-        if (m == NEG_INF || mt > m + LAZY2) mr = fmaxf(m, mt);
-        float cf = (m == NEG_INF) ? 1.f : exp2f(m - mr);
-        if (__any(cf != 1.f)) {
+    }
+
+    // softmax role: thread (srow, sq) owns keys 4sq .. 4sq+3 of row srow; the row's 16 threads keep identical m, l
+    const int srow = tid >> 4, sq = tid & 15;
+    const int vis = n + (srow >> 3);  // row srow sees keys < vis
+    float m_run = NEG_INF, l_run = 0.f;
+    f32x16 O = f32x16{};
+
+    auto stage = [&](int j, StageRegs& R, StageRegs& Rnext2, auto steady) {
+        // two stages in flight while this one is computed (unconditional in the steady loop: branches around loads
+        // make the compiler's wait counts pessimistic)
+        if (decltype(steady)::value || j + 2 < nst) load(j + 2, Rnext2);
+        const int k0 = cs + j * KPS;
+        f32x4 s4[2] = {f32x4{}, f32x4{}};
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float f = __shfl(cf, 8 * (i >> 2) + 4 * h + (i & 3));
+        for (int s = 0; s < 4; s++) {
+            s4[0] = mfma16(R.k[s], qb[0][s], s4[0]);
+            s4[1] = mfma16(R.k[s], qb[1][s], s4[1]);
+        }
 #pragma unroll
-                for (int nb = 0; nb < 8; nb++) O[nb][i] *= f;
+        for (int hb = 0; hb < 2; hb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) ss[dh][16 * hb + l16][16 * kq + 4 * g4 + i] = s4[hb][i];
+        lds_barrier();
+
+        // online softmax with the lazy reference max of attn_dmx (dmx.rs:72-86), log2 units
+        float sv[4], mt = NEG_INF;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int key = k0 + 4 * sq + i;
+            const float x = (ss[0][srow][4 * sq + i] + ss[1][srow][4 * sq + i]) * scale2;
+            sv[i] = (key < vis && key >= start) ? x : NEG_INF;
+            mt = fmaxf(mt, sv[i]);
+        }
+        mt = reduce16(mt, [](float a, float b) { return fmaxf(a, b); });
+        float mr = m_run;
+        if (m_run == NEG_INF || mt > m_run + LAZY2) mr = fmaxf(m_run, mt);
+        const float cf = m_run == NEG_INF ? 1.f : exp2f(m_run - mr);
+        float psum = 0.f;
+        _Float16 p4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            p4[i] = (_Float16)(sv[i] > NEG_INF ? exp2f(sv[i] - mr) : 0.f);
+            psum += (float)p4[i];
+        }
+        *(uint2*)&ps[srow][4 * sq] = *(const uint2*)p4;
+        psum = reduce16(psum, [](float a, float b) { return a + b; });
+        l_run = l_run * cf + psum;
+        m_run = mr;
+        if (sq == 0) cfs[srow] = cf;
+        lds_barrier();
+
+        if (__any(cfs[r] != 1.f)) {
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const float4 f = *(const float4*)&cfs[8 * a + 4 * h];
+                O[4 * a] *= f.x;
+                O[4 * a + 1] *= f.y;
+                O[4 * a + 2] *= f.z;
+                O[4 * a + 3] *= f.w;
             }
         }
-        lsum *= cf;
-        m = mr;
-        half8 pa[2];
+        const bool tail = k0 + KPS > kend;  // V rows past the written length may hold anything: keep 0 * V finite
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            float p = S[i] > NEG_INF ? exp2f(S[i] - mr) : 0.f;
-            _Float16 ph = (_Float16)p;
-            lsum += (float)ph;
-            pa[i >> 3][i & 7] = ph;
+        for (int s2 = 0; s2 < KPS / 16; s2++) {
+            const half8 pa = *(const half8*)&ps[r][16 * s2 + 8 * h];
+            half8 vb = R.v[s2];
+            if (tail) {
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++)
+                    if (k0 + 16 * s2 + 8 * h + jj >= kend) vb[jj] = (_Float16)0.f;
+            }
+            O = mfma32(pa, vb, O);
         }
-        if (k0 + 32 > kend) {  // tail tile: V rows past the written length may hold anything; keep 0 * V finite
-#pragma unroll
-            for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-                    if (k0 + 16 * s2 + 8 * h + j >= kend)
-#pragma unroll
-                        for (int nb = 0; nb < 8; nb++) va[s2][nb][j] = (_Float16)0.f;
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-            for (int nb = 0; nb < 8; nb++) O[nb] = mfma32(pa[s2], va[s2][nb], O[nb]);
+    };
+    // register sets rotate with period 3: (this stage, stage + 2) = (A, C), (B, A), (C, B)
+    int j = 0;
+    for (; j + 5 <= nst; j += 3) {
+        stage(j, RA, RC, std::true_type{});
+        stage(j + 1, RB, RA, std::true_type{});
+        stage(j + 2, RC, RB, std::true_type{});
     }
-    lsum += __shfl_xor(lsum, 32);
+    if (j < nst) stage(j, RA, RC, std::false_type{});
+    if (j + 1 < nst) stage(j + 1, RB, RA, std::false_type{});
+    if (j + 2 < nst) stage(j + 2, RC, RB, std::false_type{});
+    if (j + 3 < nst) stage(j + 3, RA, RC, std::false_type{});
 
-    // merge the 4 waves
-    __shared__ float sm_m[4][32], sm_l[4][32];
-    __shared__ float so[32][HD + 4];
-    if (h == 0) {
-        sm_m[w][r] = m;
-        sm_l[w][r] = lsum;
-    }
-    __syncthreads();
+    // partials: this wave's 32 dims of every row of a present token; m and l from the rows' softmax threads
+    const int nrows = 8 * ntok;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        int ri = 8 * (i >> 2) + 4 * h + (i & 3);
-        float M = fmaxf(fmaxf(sm_m[0][ri], sm_m[1][ri]), fmaxf(sm_m[2][ri], sm_m[3][ri]));
-        float mw = sm_m[w][ri];
-        float f = mw == NEG_INF ? 0.f : exp2f(mw - M);
-#pragma unroll
-        for (int nb = 0; nb < 8; nb++) O[nb][i] *= f;
+        const int ri = 8 * (i >> 2) + 4 * h + (i & 3);
+        if (ri < nrows) part[((size_t)(kvh * ROWS + ri) * nch + c) * PART + PACC + 32 * w + r] = O[i];
     }
-    for (int ww = 0; ww < 4; ww++) {
-        if (w == ww) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                int ri = 8 * (i >> 2) + 4 * h + (i & 3);
-#pragma unroll
-                for (int nb = 0; nb < 8; nb++) {
-                    float* dst = &so[ri][32 * nb + r];
-                    *dst = ww == 0 ? O[nb][i] : *dst + O[nb][i];
-                }
-            }
-        }
-        __syncthreads();
-    }
-    const int nrows = 8 * ntok;
-    for (int row = 0; row < nrows; row++) {
-        float* p = part + ((size_t)(kvh * ROWS + row) * nch + c) * PART;
-        p[2 + threadIdx.x] = so[row][threadIdx.x];
-    }
-    if (threadIdx.x < nrows) {
-        int row = threadIdx.x;
-        float M = fmaxf(fmaxf(sm_m[0][row], sm_m[1][row]), fmaxf(sm_m[2][row], sm_m[3][row]));
-        float L = 0.f;
-        for (int ww = 0; ww < 4; ww++)
-            if (sm_m[ww][row] != NEG_INF) L += exp2f(sm_m[ww][row] - M) * sm_l[ww][row];
-        float* p = part + ((size_t)(kvh * ROWS + row) * nch + c) * PART;
-        p[0] = M;
-        p[1] = L;
+    if (sq == 0 && srow < nrows) {
+        float* p = part + ((size_t)(kvh * ROWS + srow) * nch + c) * PART;
+        p[0] = m_run;
+        p[1] = l_run;
     }
 }
 
@@ -282,7 +336,7 @@ __global__ void __launch_bounds__(256) decode_f32(const float* __restrict__ kpla
     __syncthreads();
     for (int row = 0; row < nrows; row++) {
         float* p = part + ((size_t)(kvh * ROWS + row) * nch + c) * PART;
-        p[2 + tid] = acc[row];
+        p[PACC + tid] = acc[row];
         if (tid == 0) {
             p[0] = sm_m[row];
             p[1] = sm_l[row];
@@ -290,30 +344,75 @@ __global__ void __launch_bounds__(256) decode_f32(const float* __restrict__ kpla
     }
 }
 
+// Merge of the split-K partials: work-group (token, head, quarter of the dims); its 256 threads are 16 chunk lanes x
+// 16 dim lanes (4 dims each), so every chunk's 64 dims are one coalesced 256-byte read and all chunks are in flight at
+// once; the 16 chunk lanes are then summed in LDS.
 __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ part, int n, int start, int ch,
                                                       int nch, const float* __restrict__ gate,
                                                       float* __restrict__ out) {
-    const int t = blockIdx.x / QH, head = blockIdx.x % QH, d = threadIdx.x;
+    const int t = blockIdx.x / QH, head = blockIdx.x % QH, dq = blockIdx.y, tid = threadIdx.x;
     const int kvh = head / GQA, row = t * GQA + head % GQA;
     const float* p = part + (size_t)(kvh * ROWS + row) * nch * PART;
     const int c0 = start / ch, c1 = (n + t + ch - 1) / ch;  // chunks holding a key of [start, n + t)
+    __shared__ float red[4];
+    __shared__ float4 acc4[16][16];
+    __shared__ float redl[16];
+    // one round trip: every thread loads all its chunks (at most MERGE_J) before using any
+    const int cl = tid >> 4, dl = tid & 15;
+    const int d0 = dq * 64 + dl * 4;
+    float mj[MERGE_J], lj[MERGE_J];
+    float4 aj[MERGE_J];
     float M = NEG_INF;
-    for (int c = c0; c < c1; c++) M = fmaxf(M, p[(size_t)c * PART]);
-    float L = 0.f, acc = 0.f;
-    for (int c = c0; c < c1; c++) {
-        const float* pc = p + (size_t)c * PART;
-        float mc = pc[0];
-        if (mc == NEG_INF) continue;
-        float e = exp2f(mc - M);
-        L += e * pc[1];
-        acc += e * pc[2 + d];
+#pragma unroll
+    for (int j = 0; j < MERGE_J; j++) {
+        const int c = c0 + cl + 16 * j;
+        mj[j] = NEG_INF;
+        lj[j] = 0.f;
+        aj[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < c1) {
+            const float* pc = p + (size_t)c * PART;
+            mj[j] = pc[0];
+            lj[j] = pc[1];
+            aj[j] = *(const float4*)(pc + PACC + d0);
+        }
+        M = fmaxf(M, mj[j]);
     }
-    float o = acc / L;
-    if (gate) {
-        float g = gate[((size_t)t * QH + head) * 512 + 256 + d];
-        o = o * (1.f / (1.f + expf(-g)));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    if ((tid & 63) == 0) red[tid >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float L = 0.f;
+#pragma unroll
+    for (int j = 0; j < MERGE_J; j++) {
+        const float e = mj[j] == NEG_INF ? 0.f : exp2f(mj[j] - M);
+        L += e * lj[j];
+        acc.x += e * aj[j].x;
+        acc.y += e * aj[j].y;
+        acc.z += e * aj[j].z;
+        acc.w += e * aj[j].w;
     }
-    out[((size_t)t * QH + head) * HD + d] = o;
+    acc4[cl][dl] = acc;
+    if (dl == 0) redl[cl] = L;
+    __syncthreads();
+    if (tid < 64) {
+        const int dd = tid >> 2, comp = tid & 3;
+        float sum = 0.f, lt = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 v = acc4[i][dd];
+            sum += comp == 0 ? v.x : comp == 1 ? v.y : comp == 2 ? v.z : v.w;
+            lt += redl[i];
+        }
+        const int d = dq * 64 + tid;
+        float o = sum / lt;
+        if (gate) {
+            const float g = gate[((size_t)t * QH + head) * 512 + 256 + d];
+            o = o * (1.f / (1.f + expf(-g)));
+        }
+        out[((size_t)t * QH + head) * HD + d] = o;
+    }
 }
 
 }  // namespace
@@ -321,32 +420,31 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
 DecodePlan decode_plan(int n, int ntok, int start) {
     const int kend = n + ntok - 1;
     int ch = (kend + 127) / 128;  // about 128 chunks per kv head: 256 work-groups for 256 CUs
-    ch = (ch + 31) / 32 * 32;     // whole 32-key tiles
+    ch = (ch + KBLK - 1) / KBLK * KBLK;  // whole K blocks; a stage may reach 32 keys past the chunk (store slack)
     if (ch < 128) ch = 128;
     return DecodePlan{ch, (kend + ch - 1) / ch, start / ch};
 }
 
-hipError_t launch_decode_core(const Geom& g, const void* base, int layer, const float* q, int ntok, int n, int start,
-                              float scale, const DecodePlan& p, const DecodeWs& ws, hipStream_t s) {
-    if (p.nch > ws.max_chunks) return hipErrorInvalidValue;
-    const char* b = (const char*)base;
-    const void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
-    const void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
+hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float* q, int ntok, int n, int start,
+                              float scale, const DecodePlan& p, const DecodeWs& ws, const FusedAppend& fa,
+                              const Launch& L) {
+    if (p.nch > ws.max_chunks || p.nch - p.c0 > 16 * MERGE_J) return hipErrorInvalidValue;
+    char* b = (char*)base;
+    void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
+    void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
     const float scale2 = scale * LOG2E;
     dim3 grid(p.nch - p.c0, KVH);
     if (g.fmt == 0)
-        decode_f16<<<grid, 256, 0, s>>>((const _Float16*)kp, (const _Float16*)vp, g.plane_elems, q, ntok, n, start,
-                                        scale2, p.ch, p.nch, p.c0, ws.part);
-    else
-        decode_f32<<<grid, 256, 0, s>>>((const float*)kp, (const float*)vp, g.plane_elems, q, ntok, n, start, scale2,
-                                        p.ch, p.nch, p.c0, ws.part);
-    return hipGetLastError();
+        return launch(decode_f16, grid, dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.ch, p.nch,
+                      p.c0, ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
+    if (fa.ntok) return hipErrorNotSupported;
+    return launch(decode_f32, grid, dim3(256), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.ch, p.nch, p.c0,
+                  ws.part);
 }
 
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
-                               float* out, hipStream_t s) {
-    decode_combine<<<ntok * QH, 256, 0, s>>>(ws.part, n, start, p.ch, p.nch, gate, out);
-    return hipGetLastError();
+                               float* out, const Launch& L) {
+    return launch(decode_combine, dim3(ntok * QH, HD / 64), dim3(256), L, ws.part, n, start, p.ch, p.nch, gate, out);
 }
 
 }  // namespace mkv

@@ -69,28 +69,34 @@ hipEvent_t take_event(mkv_store* h) {
     return e;
 }
 
-// Runs `launch` (which enqueues one kernel on h->stream), bracketed by two events when tracing.
+// Runs `fn(const Launch&)`, which enqueues one kernel on h->stream; while tracing, the kernel's own start and end
+// timestamps land in two events kept for mkv_trace_read.
 template <typename F>
-hipError_t traced(mkv_store* h, int kind, F&& launch) {
-    if (!h->tracing) return launch();
-    hipEvent_t a = take_event(h), b = take_event(h);
-    if (!a || !b) return hipErrorOutOfMemory;
-    hipError_t e = hipEventRecord(a, h->stream);
-    if (e == hipSuccess) e = launch();
-    if (e == hipSuccess) e = hipEventRecord(b, h->stream);
-    if (e == hipSuccess) h->pending.push_back({kind, a, b});
+hipError_t traced(mkv_store* h, int kind, F&& fn) {
+    Launch L{h->stream};
+    if (!h->tracing) return fn(L);
+    L.a = take_event(h);
+    L.b = take_event(h);
+    if (!L.a || !L.b) return hipErrorOutOfMemory;
+    hipError_t e = fn(L);
+    if (e == hipSuccess) {
+        h->pending.push_back({kind, L.a, L.b});
+    } else {
+        h->pool.push_back(L.a);
+        h->pool.push_back(L.b);
+    }
     return e;
 }
 
 hipError_t decode_all(mkv_store* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
-                      const float* gate) {
+                      const float* gate, const FusedAppend& fa = FusedAppend{}) {
     DecodePlan p = decode_plan(n, ntok, start);
-    hipError_t e = traced(h, MKV_SPAN_CORE, [&] {
-        return launch_decode_core(h->g, h->base, layer, q, ntok, n, start, scale, p, h->dws, h->stream);
+    hipError_t e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
+        return launch_decode_core(h->g, h->base, layer, q, ntok, n, start, scale, p, h->dws, fa, L);
     });
     if (e != hipSuccess) return e;
     return traced(h, MKV_SPAN_MERGE,
-                  [&] { return launch_decode_merge(ntok, n, start, p, h->dws, gate, out, h->stream); });
+                  [&](const Launch& L) { return launch_decode_merge(ntok, n, start, p, h->dws, gate, out, L); });
 }
 
 void free_events(mkv_store* h) {
@@ -125,7 +131,9 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
     h->g.plane_elems = (size_t)ctx * HD;
     h->stream = (hipStream_t)stream;
     h->len.assign(layers, 0);
-    size_t bytes = (size_t)layers * 2 * KVH * h->g.plane_bytes();
+    // + slack: a decode stage starting on a 32-position boundary reads up to 64 positions, which may reach past the
+    // last plane's end (the rows read there are masked, never used)
+    size_t bytes = (size_t)layers * 2 * KVH * h->g.plane_bytes() + STORE_SLACK;
     hipError_t e = hipMalloc(&h->base, bytes);
     if (e != hipSuccess) {
         delete h;
@@ -207,8 +215,9 @@ int mkv_append(mkv_t* h, int layer, int pos, int ntok, const float* kn, const fl
     if (pos > h->len[layer])
         return fail(MKV_E_POS, "mkv_append: position %d leaves a hole after the written length %d", pos,
                     h->len[layer]);
-    hipError_t e = traced(h, MKV_SPAN_KV_WRITE,
-                          [&] { return launch_append(h->g, h->base, layer, pos, ntok, kn, v, tab, h->stream); });
+    hipError_t e = traced(h, MKV_SPAN_KV_WRITE, [&](const Launch& L) {
+        return launch_append(h->g, h->base, layer, pos, ntok, kn, v, tab, L);
+    });
     if (e != hipSuccess) return hip_fail(e, "mkv_append");
     h->len[layer] = pos + ntok;
     return MKV_OK;
@@ -245,17 +254,48 @@ int mkv_decode(mkv_t* h, int layer, const float* q, int ntok, int n, int start, 
 int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* kn, const float* v, const float* tab,
                       const float* q, int start, float scale, float* out, const float* gate) {
     if (ntok < 1 || ntok > 4) return fail(MKV_E_ARG, "mkv_append_decode: %d tokens outside [1, 4]", ntok);
-    if (int rc = mkv_append(h, layer, n - 1, ntok, kn, v, tab)) return rc;
-    return mkv_decode(h, layer, q, ntok, n, start, scale, out, gate);
+    if (!h || !kn || !v || !tab) return fail(MKV_E_ARG, "mkv_append_decode: NULL argument");
+    if (int rc = check_layer(h, layer)) return rc;
+    const int pos = n - 1;
+    if (pos < 0 || pos + ntok > h->g.ctx)
+        return fail(MKV_E_POS, "mkv_append_decode: positions [%d, %d) outside the context %d", pos, pos + ntok,
+                    h->g.ctx);
+    if (pos > h->len[layer])
+        return fail(MKV_E_POS, "mkv_append_decode: position %d leaves a hole after the written length %d", pos,
+                    h->len[layer]);
+    if (h->g.fmt != MKV_F16) {  // f32 store: the append kernel, then the decode
+        if (int rc = mkv_append(h, layer, pos, ntok, kn, v, tab)) return rc;
+        return mkv_decode(h, layer, q, ntok, n, start, scale, out, gate);
+    }
+    const int old_len = h->len[layer];
+    h->len[layer] = pos + ntok;
+    if (int rc = check_attn(h, "mkv_append_decode", layer, q, ntok, 4, n, start, out)) {
+        h->len[layer] = old_len;
+        return rc;
+    }
+    FusedAppend fa;
+    fa.kn = kn;
+    fa.v = v;
+    fa.tab = tab;
+    fa.pos = pos;
+    fa.ntok = ntok;
+    hipError_t e = decode_all(h, layer, q, ntok, n, start, scale, out, gate, fa);
+    if (e != hipSuccess) {
+        h->len[layer] = old_len;
+        return hip_fail(e, "mkv_append_decode");
+    }
+    return MKV_OK;
 }
 
 int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, float scale, float* out,
                 const float* gate) {
     if (int rc = check_attn(h, "mkv_prefill", layer, q, T, MKV_PREFILL_MAX, n, start, out)) return rc;
-    hipError_t e = traced(h, MKV_SPAN_CORE, [&] {
-        return launch_prefill(h->g, h->base, layer, q, T, n, start, scale, out, gate, h->pws, h->pws_floats,
-                              h->stream);
+    hipError_t e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
+        return launch_prefill(h->g, h->base, layer, q, T, n, start, scale, h->pws, h->pws_floats, L);
     });
+    if (e == hipSuccess)
+        e = traced(h, MKV_SPAN_MERGE,
+                   [&](const Launch& L) { return launch_prefill_merge(T, n, start, h->pws, gate, out, L); });
     if (e == hipErrorNotSupported) {
         // no prefill kernel for this configuration: the decode kernel over groups of 4 tokens (same semantics)
         for (int t0 = 0; t0 < T; t0 += 4) {
@@ -339,7 +379,7 @@ int mkv_read_rows(mkv_t* h, int layer, int which, int p0, int p1, void* dst) {
     if (int rc = check_layer(h, layer)) return rc;
     if (which != MKV_K && which != MKV_V) return fail(MKV_E_ARG, "mkv_read_rows: which = %d", which);
     if (p0 < 0 || p1 < p0 || p1 > h->g.ctx) return fail(MKV_E_POS, "mkv_read_rows: [%d, %d)", p0, p1);
-    hipError_t e = launch_read_rows(h->g, h->base, layer, which, p0, p1, dst, h->stream);
+    hipError_t e = launch_read_rows(h->g, h->base, layer, which, p0, p1, dst, Launch{h->stream});
     return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_read_rows");
 }
 
@@ -351,7 +391,7 @@ int mkv_write_rows(mkv_t* h, int layer, int which, int p0, int p1, const void* s
     if (p0 > h->len[layer])
         return fail(MKV_E_POS, "mkv_write_rows: position %d leaves a hole after the written length %d", p0,
                     h->len[layer]);
-    hipError_t e = launch_write_rows(h->g, h->base, layer, which, p0, p1, src, h->stream);
+    hipError_t e = launch_write_rows(h->g, h->base, layer, which, p0, p1, src, Launch{h->stream});
     if (e != hipSuccess) return hip_fail(e, "mkv_write_rows");
     if (p1 > h->len[layer]) h->len[layer] = p1;
     return MKV_OK;

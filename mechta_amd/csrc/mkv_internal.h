@@ -1,10 +1,11 @@
-// mkv_internal.h -- shared definitions of libmechta_kv: store layout, kernel launchers, error plumbing.
+// mkv_internal.h -- shared definitions of libmechta_kv: store layout, launch helper, kernel launchers.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
 #include <cstdint>
-#include <string>
+#include <tuple>
 
 namespace mkv {
 
@@ -15,7 +16,9 @@ constexpr int GQA = QH / KVH;
 constexpr int KBLK = 32;     // K plane: positions per block, [pos/32][d/8][pos%32][8]
 constexpr int VGRP = 8;      // V plane: positions per group, [pos/8][d][pos%8]
 constexpr int ROWS = 32;     // query rows per KV head in decode: 4 tokens x 8 heads
-constexpr int PART = 2 + HD; // split-K partial: [m, l, acc[256]]
+constexpr int PART = 4 + HD; // split-K partial: [m, l, 0, 0, acc[256]] (acc 16-byte aligned)
+constexpr int PACC = 4;      // offset of acc in a partial
+constexpr size_t STORE_SLACK = 64 * HD * 4;  // bytes allocated past the last plane (see mkv_create)
 
 // Element offset of (pos, d) inside one f16 K plane.
 __host__ __device__ inline size_t k_off(int pos, int d) {
@@ -24,6 +27,31 @@ __host__ __device__ inline size_t k_off(int pos, int d) {
 // Element offset of (pos, d) inside one f16 V plane.
 __host__ __device__ inline size_t v_off(int pos, int d) {
     return (size_t)(pos / VGRP) * (VGRP * HD) + (size_t)d * VGRP + (pos % VGRP);
+}
+
+// f32 -> f16 bits: v_cvt_f16_f32 rounds to nearest even and keeps subnormals.
+__device__ inline unsigned short f2h(float x) {
+    _Float16 h = (_Float16)x;
+    return __builtin_bit_cast(unsigned short, h);
+}
+
+// NEOX RoPE value of dim d of one 256-dim K row a, table tb = [cos 0..31 | sin 0..31] (kv_src, kv.wgsl:19-23):
+// d < 32: a[d]c[d] - a[d+32]s[d]; 32 <= d < 64 (i = d - 32): a[i]s[i] + a[d]c[i]; else a[d].
+// Every product and the sum are rounded to f32 separately (no FMA contraction).
+__device__ inline float rope_dim(const float* __restrict__ a, const float* __restrict__ tb, int d) {
+#pragma clang fp contract(off)
+    if (d < 32) {
+        float p1 = a[d] * tb[d];
+        float p2 = a[d + 32] * tb[32 + d];
+        return p1 - p2;
+    }
+    if (d < 64) {
+        int i = d - 32;
+        float p1 = a[i] * tb[32 + i];
+        float p2 = a[d] * tb[i];
+        return p1 + p2;
+    }
+    return a[d];
 }
 
 // Geometry of one store, passed by value to launchers.
@@ -36,30 +64,60 @@ struct Geom {
     size_t plane(int layer, int which, int kvh) const { return ((size_t)layer * 2 + which) * KVH + kvh; }
 };
 
+// Where and how a kernel is launched: the stream, and two events that (when set) take the kernel's start and end
+// timestamps from its dispatch packet (hipExtLaunchKernel), so traced kernel times are the kernels' own durations.
+struct Launch {
+    hipStream_t s;
+    hipEvent_t a = nullptr, b = nullptr;
+};
+
+template <typename... P, typename... A>
+hipError_t launch(void (*k)(P...), dim3 grid, dim3 block, const Launch& L, A... a) {
+    static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+    std::tuple<P...> t{static_cast<P>(a)...};
+    void* args[sizeof...(P) > 0 ? sizeof...(P) : 1];
+    std::apply([&](auto&... x) {
+        int i = 0;
+        ((args[i++] = (void*)&x), ...);
+    }, t);
+    return hipExtLaunchKernel((const void*)k, grid, block, args, 0, L.s, L.a, L.b, 0);
+}
+
 // Decode workspace: partials of the split-K decode.
 struct DecodeWs {
     float* part;      // [KVH*ROWS][max_chunks][PART]
     int max_chunks;
 };
 
+// Rows appended by the decode kernel itself (mkv_append_decode): ntok = 0 for none.
+struct FusedAppend {
+    const float* kn = nullptr;  // [ntok][2][256]
+    const float* v = nullptr;   // [ntok][512]
+    const float* tab = nullptr; // [ntok][64]
+    int pos = 0, ntok = 0;
+};
+
 // ---- launchers (kernels live in kv_append.hip, kv_decode.hip, kv_prefill.hip) ----
 hipError_t launch_append(const Geom& g, void* base, int layer, int pos, int ntok, const float* kn, const float* v,
-                         const float* tab, hipStream_t s);
+                         const float* tab, const Launch& L);
 hipError_t launch_read_rows(const Geom& g, const void* base, int layer, int which, int p0, int p1, void* dst,
-                            hipStream_t s);
+                            const Launch& L);
 hipError_t launch_write_rows(const Geom& g, void* base, int layer, int which, int p0, int p1, const void* src,
-                             hipStream_t s);
-// Split-K pass and merge of the decode (two kernels, both on stream s).
+                             const Launch& L);
+// Split-K pass and merge of the decode (two kernels).
 struct DecodePlan {
     int ch, nch, c0;
 };
 DecodePlan decode_plan(int n, int ntok, int start);
-hipError_t launch_decode_core(const Geom& g, const void* base, int layer, const float* q, int ntok, int n, int start,
-                              float scale, const DecodePlan& p, const DecodeWs& ws, hipStream_t s);
+hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float* q, int ntok, int n, int start,
+                              float scale, const DecodePlan& p, const DecodeWs& ws, const FusedAppend& fa,
+                              const Launch& L);
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
-                               float* out, hipStream_t s);
+                               float* out, const Launch& L);
+// Prefill: hipErrorNotSupported when the configuration has no prefill kernel (the caller then uses the decode).
 hipError_t launch_prefill(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
-                          float scale, float* out, const float* gate, float* ws, size_t ws_floats, hipStream_t s);
+                          float scale, float* ws, size_t ws_floats, const Launch& L);
+hipError_t launch_prefill_merge(int T, int n, int start, float* ws, const float* gate, float* out, const Launch& L);
 size_t prefill_ws_floats(int ctx);
 
 }  // namespace mkv
