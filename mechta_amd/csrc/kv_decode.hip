@@ -20,45 +20,14 @@
 // Partials keep m in log2 units (scores are pre-multiplied by scale * log2 e).
 #include <type_traits>
 
-#include "mkv_internal.h"
+#include "mkv_device.h"
 
 namespace mkv {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
-
-constexpr float LOG2E = 1.4426950408889634f;
-constexpr float LAZY2 = 8.0f * LOG2E;  // DM_LAZY = 8 (dmx.rs:124) in log2 units
-constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr int KPS = 64;                        // keys per stage of the decode ring
 constexpr int PS_STRIDE = KPS + 8;             // halves per P row in LDS (conflict-free 16-byte reads)
 constexpr int MERGE_J = 9;  // chunks per merge lane: 16 lanes x 9 >= the at most 130 chunks of decode_plan
-
-__device__ inline f32x16 mfma32(half8 a, half8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ inline f32x4 mfma16(half8 a, half8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// Reduction over the 16 lanes of a DPP row (a row of S): quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
-// row_mirror -- lane swaps inside the ALU, no LDS round trip.
-template <typename Op>
-__device__ inline float reduce16(float x, Op op) {
-    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true)));
-    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true)));
-    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true)));
-    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true)));
-    return x;
-}
-
-// Work-group barrier for LDS traffic only: waits for this wave's LDS operations, not for its global loads (a
-// __syncthreads() would also wait for every pending global load and drain the prefetched stages).
-__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // One stage of this wave's registers: K operands (16 keys x 128 dims) and V operands (64 keys x 32 dims).
 struct StageRegs {
@@ -176,7 +145,7 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
         for (int i = 0; i < 4; i++) {
             const int key = k0 + 4 * sq + i;
             const float x = (ss[0][srow][4 * sq + i] + ss[1][srow][4 * sq + i]) * scale2;
-            sv[i] = (key < vis && key >= start) ? x : NEG_INF;
+            sv[i] = (key < vis && key >= start && key < ce) ? x : NEG_INF;  // a stage may reach into the next chunk
             mt = fmaxf(mt, sv[i]);
         }
         mt = reduce16(mt, [](float a, float b) { return fmaxf(a, b); });
@@ -347,12 +316,12 @@ __global__ void __launch_bounds__(256) decode_f32(const float* __restrict__ kpla
 // Merge of the split-K partials: work-group (token, head, quarter of the dims); its 256 threads are 16 chunk lanes x
 // 16 dim lanes (4 dims each), so every chunk's 64 dims are one coalesced 256-byte read and all chunks are in flight at
 // once; the 16 chunk lanes are then summed in LDS.
-__global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ part, int n, int start, int ch,
-                                                      int nch, const float* __restrict__ gate,
+__global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ part, int rpk, int n, int start,
+                                                      int ch, int nch, const float* __restrict__ gate,
                                                       float* __restrict__ out) {
     const int t = blockIdx.x / QH, head = blockIdx.x % QH, dq = blockIdx.y, tid = threadIdx.x;
     const int kvh = head / GQA, row = t * GQA + head % GQA;
-    const float* p = part + (size_t)(kvh * ROWS + row) * nch * PART;
+    const float* p = part + ((size_t)kvh * rpk + row) * nch * PART;
     const int c0 = start / ch, c1 = (n + t + ch - 1) / ch;  // chunks holding a key of [start, n + t)
     __shared__ float red[4];
     __shared__ float4 acc4[16][16];
@@ -442,9 +411,15 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
                   ws.part);
 }
 
+hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int ch, int nch, const float* gate,
+                        float* out, const Launch& L) {
+    if (nch - start / ch > 16 * MERGE_J) return hipErrorInvalidValue;
+    return launch(decode_combine, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, ch, nch, gate, out);
+}
+
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
                                float* out, const Launch& L) {
-    return launch(decode_combine, dim3(ntok * QH, HD / 64), dim3(256), L, ws.part, n, start, p.ch, p.nch, gate, out);
+    return launch_merge(ws.part, ROWS, ntok, n, start, p.ch, p.nch, gate, out, L);
 }
 
 }  // namespace mkv

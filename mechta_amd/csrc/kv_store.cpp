@@ -142,9 +142,7 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
     }
     h->dws.max_chunks = ctx / 128 + 2;
     size_t dws_bytes = (size_t)KVH * ROWS * h->dws.max_chunks * PART * sizeof(float);
-    h->pws_floats = prefill_ws_floats(ctx);
     e = hipMalloc(&h->dws.part, dws_bytes);
-    if (e == hipSuccess && h->pws_floats) e = hipMalloc(&h->pws, h->pws_floats * sizeof(float));
     if (e != hipSuccess) {
         (void)hipGetLastError();
         (void)hipFree(h->base);
@@ -290,19 +288,36 @@ int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* kn, con
 int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, float scale, float* out,
                 const float* gate) {
     if (int rc = check_attn(h, "mkv_prefill", layer, q, T, MKV_PREFILL_MAX, n, start, out)) return rc;
-    hipError_t e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
-        return launch_prefill(h->g, h->base, layer, q, T, n, start, scale, h->pws, h->pws_floats, L);
-    });
-    if (e == hipSuccess)
-        e = traced(h, MKV_SPAN_MERGE,
-                   [&](const Launch& L) { return launch_prefill_merge(T, n, start, h->pws, gate, out, L); });
-    if (e == hipErrorNotSupported) {
-        // no prefill kernel for this configuration: the decode kernel over groups of 4 tokens (same semantics)
-        for (int t0 = 0; t0 < T; t0 += 4) {
+    hipError_t e = hipSuccess;
+    if (h->g.fmt == MKV_F16) {
+        const PrefillPlan p = prefill_plan(T, n);
+        const size_t need = prefill_ws_floats(T, p.nch);
+        if (need > h->pws_floats) {  // partials of the largest prefill so far; grown on demand
+            e = hipStreamSynchronize(h->stream);
+            if (e == hipSuccess && h->pws) e = hipFree(h->pws);
+            h->pws = nullptr;
+            h->pws_floats = 0;
+            if (e == hipSuccess) e = hipMalloc(&h->pws, need * sizeof(float));
+            if (e != hipSuccess) {
+                h->pws = nullptr;
+                (void)hipGetLastError();
+                return fail(MKV_E_NOMEM, "mkv_prefill: %zu bytes of split-K partials", need * sizeof(float));
+            }
+            h->pws_floats = need;
+        }
+        e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
+            return launch_prefill(h->g, h->base, layer, q, T, n, start, scale, p, h->pws, L);
+        });
+        if (e == hipSuccess)
+            e = traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {
+                return launch_merge(h->pws, T * GQA, T, n, start, p.ch, p.nch, gate, out, L);
+            });
+    } else {
+        // f32 store: exact f32 attention of the decode kernel, 4 tokens per launch (each token's causal window)
+        for (int t0 = 0; t0 < T && e == hipSuccess; t0 += 4) {
             int nt = T - t0 < 4 ? T - t0 : 4;
             e = decode_all(h, layer, q + (size_t)t0 * QH * HD, nt, n + t0, start, scale, out + (size_t)t0 * QH * HD,
                            gate ? gate + (size_t)t0 * QH * 512 : nullptr);
-            if (e != hipSuccess) break;
         }
     }
     return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_prefill");

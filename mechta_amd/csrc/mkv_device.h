@@ -1,0 +1,57 @@
+// mkv_device.h -- device helpers shared by the attention kernels (gfx950).
+#pragma once
+#include "mkv_internal.h"
+
+namespace mkv {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LAZY2 = 8.0f * LOG2E;  // DM_LAZY = 8 (dmx.rs:124) in log2 units
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+__device__ inline f32x16 mfma32(half8 a, half8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ inline f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Key offset inside a 32-key K block of the key loaded by A-operand row m of the 32x32 MFMA. The C layout of that
+// MFMA gives lane half h the rows 8a + 4h + b (register 4a + b); loading row m from key perm(m) makes register i of
+// lane half h hold key 8h + i (i < 8) or 16 + 8h + (i - 8) (i >= 8): exactly the keys the A operand (P) of the
+// following P.V MFMA needs in that lane, so S^T = K.Q^T turns into P without leaving the registers.
+__device__ inline int key_perm(int m) {
+    int a = m >> 3, c = (m >> 2) & 1, b = m & 3;
+    return 16 * (a >> 1) + 8 * c + 4 * (a & 1) + b;
+}
+
+// Reduction over the 16 lanes of a DPP row: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror
+// (lane swaps inside the ALU, no LDS round trip).
+template <typename Op>
+__device__ inline float reduce16(float x, Op op) {
+    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true)));
+    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true)));
+    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true)));
+    x = op(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true)));
+    return x;
+}
+
+// Work-group barrier for LDS traffic only: waits for this wave's LDS operations, not for its global loads (a
+// __syncthreads() would also wait for every pending global load and drain the loads already in flight).
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Direct global -> LDS load of 64 lanes x 16 bytes: lane i's 16 bytes from src land at lds_base + 16i. Issued as
+// inline assembly, so the compiler neither counts it nor orders LDS reads behind it: every wait for these loads is
+// an explicit s_waitcnt in the caller (the compiler's own waits for its loads stay correct, they only wait longer).
+__device__ inline void dma16(const void* src, void* lds_base) {
+    const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void*)lds_base);  // wave-uniform
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+}  // namespace mkv

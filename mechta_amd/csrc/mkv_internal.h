@@ -114,10 +114,17 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
                               const Launch& L);
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
                                float* out, const Launch& L);
-// Prefill: hipErrorNotSupported when the configuration has no prefill kernel (the caller then uses the decode).
+// Merge of split-K partials laid out [kvh][row < rpk][chunk < nch][PART], row = token*8 + head of the kv head:
+// out[t][head] for t < ntok over the chunks of ch positions holding a key of [start, n + t), optional output gate.
+hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int ch, int nch, const float* gate,
+                        float* out, const Launch& L);
+// Prefill (f16 store): split-K pass into the partials ws, then launch_merge with the returned plan.
+struct PrefillPlan {
+    int ch, nch;  // positions per split, splits
+};
+PrefillPlan prefill_plan(int T, int n);
+size_t prefill_ws_floats(int T, int nch);
 hipError_t launch_prefill(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
-                          float scale, float* ws, size_t ws_floats, const Launch& L);
-hipError_t launch_prefill_merge(int T, int n, int start, float* ws, const float* gate, float* out, const Launch& L);
-size_t prefill_ws_floats(int ctx);
+                          float scale, const PrefillPlan& p, float* ws, const Launch& L);
 
 }  // namespace mkv

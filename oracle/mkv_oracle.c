@@ -241,6 +241,10 @@ static void dmx_unit(const uint16_t* kc, const uint16_t* vc, const float* qh /*[
         int k0 = cs + tile * 64;
         /* S = Q K^T on f16 operands, f32 sums */
         for (int j = 0; j < 64; j++) {
+            if (k0 + j >= lim) { /* past every row's window: masked below; not read (the array may end here) */
+                for (int r = 0; r < m; r++) S[r][j] = 0.0f;
+                continue;
+            }
             size_t kb = (size_t)(k0 + j) * ORC_ROW + (size_t)kvh * ORC_D;
             float kr[ORC_D];
             for (int d = 0; d < ORC_D; d++) kr[d] = orc_f16_to_f32(kc[kb + d]);
@@ -276,6 +280,7 @@ static void dmx_unit(const uint16_t* kc, const uint16_t* vc, const float* qh /*[
         }
         /* O += P V (f16 P, f16 V, f32 sums) */
         for (int j = 0; j < 64; j++) {
+            if (k0 + j >= lim) continue; /* P = 0 for every row */
             size_t vb = (size_t)(k0 + j) * ORC_ROW + (size_t)kvh * ORC_D;
             float vr[ORC_D];
             for (int d = 0; d < ORC_D; d++) vr[d] = orc_f16_to_f32(vc[vb + d]);

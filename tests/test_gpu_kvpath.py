@@ -150,6 +150,8 @@ def test_errors(torch_gpu, mk):
 DECODE_CASES = [  # (ctx, n0 positions already in the cache, ntok, start)
     (4096, 1, 1, 0), (4096, 31, 4, 0), (4096, 300, 4, 0), (4096, 1000, 1, 0), (4096, 4092, 4, 0),
     (8192, 4096, 1, 0), (8192, 5000, 4, 0), (8192, 2047, 2, 0), (8192, 3000, 3, 1), (8192, 3000, 4, 700),
+    # chunk sizes that are not a multiple of the 64-key stage (the last stage of a chunk reaches into the next one)
+    (20480, 20000, 4, 0), (20480, 17000, 1, 0),
 ]
 
 
@@ -267,3 +269,39 @@ def test_snapshot_roundtrip(torch_gpu, mk, fmt, p):
             assert np.array_equal(kb, rows_a[l][0]) and np.array_equal(vb, rows_a[l][1])
             ob = b.append_decode(l, p + 1, dev(torch, kn), dev(torch, v), dev(torch, tab), q).cpu().numpy()
             assert np.array_equal(ob, outs_a[l]), f"layer {l}: outputs differ after restore"
+
+
+# ------------------------------------------------------------------------------------------------ full sizes -----
+
+def test_decode_cfg2_full_size(torch_gpu, mk):
+    """4-token verify on an f16 cache at 65,536 positions, append through the fused entry,
+    then 2 drafts rolled back and the next step appended over them; both steps against the oracle."""
+    torch = torch_gpu
+    print("decode cfg2 full size", flush=True)
+    n0, ctx = 65536, 66560
+    with mk.KvStore(1, ctx, F16) as st:
+        fill(torch, st, 0, F16, n0, seed=900)
+        for step, pos in enumerate((n0, n0 + 2)):
+            kn, v = kv_inputs(901 + step, 4)
+            q = q_inputs(911 + step, 4)
+            out = st.append_decode(0, pos + 1, dev(torch, kn), dev(torch, v), dev(torch, O.rope_tables(pos, 4)),
+                                   dev(torch, q)).cpu().numpy()
+            kc, vc = caches_np(st, 0, pos + 4)
+            assert_attn_close(out, O.attn_dmx(kc, vc, q, pos + 1), what=f"cfg2 step {step}")
+            st.set_len(pos + 2)  # 2 drafts rejected
+
+
+def test_prefill_cfg3_sampled_tokens(torch_gpu, mk):
+    """512 tokens appended to a cache at 28,000 positions, Q pre-scaled by 1/16 (scale 1),
+    causal over 28,512 keys; the oracle checks 12 sampled tokens (first, last, around 64-token groups)."""
+    torch = torch_gpu
+    print("prefill cfg3 sampled", flush=True)
+    n0, T = 28000, 512
+    with mk.KvStore(1, 28672, F16) as st:
+        fill(torch, st, 0, F16, n0 + T, seed=950)
+        q = q_inputs(951, T) / 16.0
+        out = st.prefill(0, dev(torch, q), n0 + 1, scale=1.0).cpu().numpy()
+        kc, vc = caches_np(st, 0, n0 + T)
+    sel = np.array([0, 1, 15, 16, 63, 64, 200, 255, 256, 400, 510, 511], np.int32)
+    ref = O.attn_fa_mx(kc, vc, q, n0 + 1, scale=1.0, sel=sel)
+    assert_attn_close(out[sel], ref, what="cfg3 prefill")
