@@ -13,6 +13,8 @@ CSRC = os.path.join(HERE, "csrc")
 OUTDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(OUTDIR, "libmechta_kv.so")
 SOURCES = ["kv_store.cpp", "kv_append.hip", "kv_decode.hip", "kv_prefill.hip"]
+# prefill: MFMA accumulators in VGPRs, so the rare lazy rescale of O is plain VALU work instead of AGPR round trips
+EXTRA = {"kv_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 ARCH = os.environ.get("MKV_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -24,7 +26,7 @@ def _compile(src, verbose):
     obj = os.path.join(OUTDIR, "obj", os.path.splitext(src)[0] + ".o")
     os.makedirs(os.path.dirname(obj), exist_ok=True)
     lang = ["-x", "hip"]
-    cmd = [HIPCC] + FLAGS + lang + ["-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC] + FLAGS + EXTRA.get(src, []) + lang + ["-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

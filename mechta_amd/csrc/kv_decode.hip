@@ -27,6 +27,7 @@ namespace {
 
 constexpr int KPS = 64;                        // keys per stage of the decode ring
 constexpr int PS_STRIDE = KPS + 8;             // halves per P row in LDS (conflict-free 16-byte reads)
+constexpr int MERGE_FEW = 16;  // chunks of the one-lane-per-dim merge
 constexpr int MERGE_J = 9;  // chunks per merge lane: 16 lanes x 9 >= the at most 130 chunks of decode_plan
 
 // One stage of this wave's registers: K operands (16 keys x 128 dims) and V operands (64 keys x 32 dims).
@@ -384,6 +385,44 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
     }
 }
 
+// Merge for few chunks (prefill splits): work-group = (token, head), thread = dim; all chunks of the row are loaded
+// in one round trip.
+__global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part, int rpk, int n, int start, int ch,
+                                                 int nch, const float* __restrict__ gate, float* __restrict__ out) {
+    const int t = blockIdx.x / QH, head = blockIdx.x % QH, d = threadIdx.x;
+    const int kvh = head / GQA, row = t * GQA + head % GQA;
+    const float* p = part + ((size_t)kvh * rpk + row) * nch * PART;
+    const int c0 = start / ch, c1 = (n + t + ch - 1) / ch;
+    float mj[MERGE_FEW], lj[MERGE_FEW], aj[MERGE_FEW];
+    float M = NEG_INF;
+#pragma unroll
+    for (int j = 0; j < MERGE_FEW; j++) {
+        const int c = c0 + j;
+        mj[j] = NEG_INF;
+        lj[j] = aj[j] = 0.f;
+        if (c < c1) {
+            const float* pc = p + (size_t)c * PART;
+            mj[j] = pc[0];
+            lj[j] = pc[1];
+            aj[j] = pc[PACC + d];
+        }
+        M = fmaxf(M, mj[j]);
+    }
+    float L = 0.f, acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < MERGE_FEW; j++) {
+        const float e = mj[j] == NEG_INF ? 0.f : exp2f(mj[j] - M);
+        L += e * lj[j];
+        acc += e * aj[j];
+    }
+    float o = acc / L;
+    if (gate) {
+        const float g = gate[((size_t)t * QH + head) * 512 + 256 + d];
+        o = o * (1.f / (1.f + expf(-g)));
+    }
+    out[((size_t)t * QH + head) * HD + d] = o;
+}
+
 }  // namespace
 
 DecodePlan decode_plan(int n, int ntok, int start) {
@@ -414,6 +453,8 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
 hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int ch, int nch, const float* gate,
                         float* out, const Launch& L) {
     if (nch - start / ch > 16 * MERGE_J) return hipErrorInvalidValue;
+    if (nch - start / ch <= MERGE_FEW)
+        return launch(merge_few, dim3(ntok * QH), dim3(256), L, part, rpk, n, start, ch, nch, gate, out);
     return launch(decode_combine, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, ch, nch, gate, out);
 }
 

@@ -3,14 +3,14 @@
 // Replaces q_f16 + attn_fa_mx + attn_fd_combine of the reference's prefill (fa_mx.wgsl:19-115, 313-319;
 // engine.rs:1215-1236). Token t of the block (0-based) sees positions [start, n + t).
 //
-// Work-group = (16 tokens of the block, split of `ch` positions, kv head): 4 waves, each owns 4 tokens x the kv
-// head's 8 query heads = 32 query rows (row = token*8 + head). The split's 32-key tiles (a 16 KB K block and four
-// 4 KB V groups, contiguous in HBM) stream through a 4-slot LDS ring filled by direct global->LDS loads, shared by
-// the 4 waves. Per tile and wave:
+// Work-group = (32 tokens of the block, split of `ch` positions, kv head): 8 waves (two per SIMD, so one wave's
+// softmax overlaps the other's matrix work), each owns 4 tokens x the kv head's 8 query heads = 32 query rows
+// (row = token*8 + head). The split's 32-key tiles (a 16 KB K block and four 4 KB V groups, contiguous in HBM)
+// stream through a 4-slot LDS ring filled by direct global->LDS loads, shared by the 8 waves. Per tile and wave:
 //   S^T[32 keys][32 rows] = K . Q^T    16 x v_mfma_f32_32x32x16_f16 (A = K rows in key_perm order from LDS,
 //                                      B = Q rounded to f16, held in registers for the whole split)
 //   online softmax of the 32 rows in registers, lazy reference max (moves when first or when the tile max exceeds
-//   it by more than 8), P rounded to f16
+//   it by more than 8), row sums from the f32 P (as attn_fa_mx), P rounded to f16 for the matrix units
 //   O[32 rows][256] += P . V           16 x v_mfma_f32_32x32x16_f16 (A = P straight from the S registers,
 //                                      B = V from LDS)
 // Each wave writes one partial [m, l, acc[256]] per row; launch_merge combines the splits (and applies the gate).
@@ -19,25 +19,27 @@
 namespace mkv {
 namespace {
 
-constexpr int PT = 16;                        // tokens per work-group
+constexpr int RB = 1;                         // 32-row blocks (4 tokens x 8 heads) per wave
+constexpr int NW = 8;                          // waves per work-group (2 per SIMD)
+constexpr int PT = NW * 4 * RB;               // tokens per work-group
 constexpr int TILE_BYTES = 32 * HD * 2;       // one 32-key K block (or its 4 V groups), f16
 constexpr int SLOT_BYTES = 2 * TILE_BYTES;    // K + V of a tile
 constexpr int NSLOT = 4;                      // LDS ring: 3 tiles in flight while one is computed
 
-__device__ inline void wait_tiles(int later) {  // at most `later` tiles (8 direct loads each) still pending
-    if (later >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (later == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+__device__ inline void wait_tiles(int later) {  // at most `later` tiles (4 direct loads each per wave) pending
+    if (later >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (later == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-__global__ void __launch_bounds__(256) prefill_f16(const _Float16* __restrict__ kplane,
+__global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restrict__ kplane,
                                                    const _Float16* __restrict__ vplane, size_t plane_elems,
                                                    const float* __restrict__ q, int T, int n, int start, float scale2,
                                                    int ch, int nch, float* __restrict__ part) {
     const int rb = blockIdx.x, sp = blockIdx.y, kvh = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int h = lane >> 5, r = lane & 31;
-    const int t0 = rb * PT + 4 * w;          // this wave's first token
+    const int t0 = rb * PT + 4 * RB * w;     // this wave's first token; row block b holds tokens t0 + 4b .. +3
     const int tlast = min(T - 1, rb * PT + PT - 1);
     const int kend = n + T - 1;              // positions written for this block
     const int cs = sp * ch, ce = min(cs + ch, n + tlast);
@@ -47,111 +49,148 @@ __global__ void __launch_bounds__(256) prefill_f16(const _Float16* __restrict__ 
 
     __shared__ __attribute__((aligned(16))) unsigned char ring[NSLOT * SLOT_BYTES];
     const int ntiles = (ce - cs + 31) / 32;
-    auto issue = [&](int j) {  // each wave copies a quarter of tile j's K block and V groups into slot j % NSLOT
+    auto issue = [&](int j) {  // each wave copies 1/NW of tile j's K block and V groups into slot j % NSLOT
+        constexpr int PART_BYTES = TILE_BYTES / NW;
         const int k0 = cs + 32 * j;
-        const unsigned char* ks = (const unsigned char*)(K + (size_t)(k0 / KBLK) * (KBLK * HD)) + w * 4096 + lane * 16;
-        const unsigned char* vs = (const unsigned char*)(V + (size_t)(k0 / VGRP) * (VGRP * HD)) + w * 4096 + lane * 16;
-        unsigned char* dst = ring + (j % NSLOT) * SLOT_BYTES + w * 4096;
+        const unsigned char* ks =
+            (const unsigned char*)(K + (size_t)(k0 / KBLK) * (KBLK * HD)) + w * PART_BYTES + lane * 16;
+        const unsigned char* vs =
+            (const unsigned char*)(V + (size_t)(k0 / VGRP) * (VGRP * HD)) + w * PART_BYTES + lane * 16;
+        unsigned char* dst = ring + (j % NSLOT) * SLOT_BYTES + w * PART_BYTES;
 #pragma unroll
-        for (int i = 0; i < 4; i++) dma16(ks + i * 1024, dst + i * 1024);
+        for (int i = 0; i < PART_BYTES / 1024; i++) dma16(ks + i * 1024, dst + i * 1024);
 #pragma unroll
-        for (int i = 0; i < 4; i++) dma16(vs + i * 1024, dst + TILE_BYTES + i * 1024);
+        for (int i = 0; i < PART_BYTES / 1024; i++) dma16(vs + i * 1024, dst + TILE_BYTES + i * 1024);
     };
     for (int j = 0; j < NSLOT - 1 && j < ntiles; j++) issue(j);
 
-    // Q as the B operand of S^T: lane (r, h) holds row r, dims 16s + 8h .. +7 for step s, rounded to f16 (q_f16);
-    // rows of tokens past the block are zero
-    const int tr = t0 + (r >> 3);
-    half8 qb[16];
-    {
+    // Q as the B operand of S^T: for row block b, lane (r, h) holds row r (token t0 + 4b + r/8, head r%8), dims
+    // 16s + 8h .. +7 for step s, rounded to f16 (q_f16); rows of tokens past the block are zero
+    half8 qb[RB][16];
+    int vis[RB];
+#pragma unroll
+    for (int b = 0; b < RB; b++) {
+        const int tr = t0 + 4 * b + (r >> 3);
+        vis[b] = tr < T ? n + tr : 0;  // row r of block b sees keys < vis[b]
         const float* qrow = q + ((size_t)min(tr, T - 1) * QH + kvh * GQA + (r & 7)) * HD + 8 * h;
 #pragma unroll
         for (int s = 0; s < 16; s++) {
             float4 x0 = *(const float4*)(qrow + 16 * s), x1 = *(const float4*)(qrow + 16 * s + 4);
             if (tr >= T) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
-            qb[s] = half8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
-                          (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
+            qb[b][s] = half8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
+                             (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
         }
     }
-    const int vis = tr < T ? n + tr : 0;  // row r sees keys < vis
     const int kaddr = h * 512 + key_perm(r) * 16;
-    float m = NEG_INF, lsum = 0.f;
-    f32x16 O[8];
+    float m[RB], lsum[RB];
+    f32x16 O[RB][8];
 #pragma unroll
-    for (int nb = 0; nb < 8; nb++) O[nb] = f32x16{};
+    for (int b = 0; b < RB; b++) {
+        m[b] = NEG_INF;
+        lsum[b] = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < 8; nb++) O[b][nb] = f32x16{};
+    }
 
+    // V rows of the tile past the written length may hold anything: zero them in LDS so that 0 * V stays finite
+    auto zero_tail = [&](int j) {
+        unsigned short* Vz = (unsigned short*)(ring + (j % NSLOT) * SLOT_BYTES + TILE_BYTES);
+        const int k0 = cs + 32 * j;
+        for (int i = tid; i < 32 * HD; i += NW * 64)
+            if (k0 + (i >> 11) * 8 + (i & 7) >= kend) Vz[i] = 0;  // group i / 2048, position i % 8 in the group
+    };
     for (int j = 0; j < ntiles; j++) {
         wait_tiles(min(ntiles - 1 - j, NSLOT - 2));
         lds_barrier();  // tile j is in LDS for every wave; every wave is done with tile j - 1
-        if (j + NSLOT - 1 < ntiles) issue(j + NSLOT - 1);
+        if (j + NSLOT - 1 < ntiles) issue(j + NSLOT - 1);  // into the slot of tile j - 1
+        const int k0 = cs + 32 * j;
+        if (k0 + 32 > kend) {
+            zero_tail(j);
+            lds_barrier();
+        }
         const unsigned char* Ks = ring + (j % NSLOT) * SLOT_BYTES;
         const unsigned char* Vs = Ks + TILE_BYTES;
-        const int k0 = cs + 32 * j;
-
-        f32x16 S = f32x16{};
+        f32x16 Scur[RB];
 #pragma unroll
-        for (int s = 0; s < 16; s++) S = mfma32(*(const half8*)(Ks + kaddr + s * 1024), qb[s], S);
-
-        float mt = NEG_INF;
+        for (int b = 0; b < RB; b++) Scur[b] = f32x16{};
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int key = k0 + 8 * h + i + (i >= 8 ? 8 : 0);
-            const float sv = S[i] * scale2;
-            S[i] = (key < vis && key >= start) ? sv : NEG_INF;
-            mt = fmaxf(mt, S[i]);
+        for (int s = 0; s < 16; s++) {
+            const half8 ka = *(const half8*)(Ks + kaddr + s * 1024);
+#pragma unroll
+            for (int b = 0; b < RB; b++) Scur[b] = mfma32(ka, qb[b][s], Scur[b]);
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        float mr = m;
-        if (m == NEG_INF || mt > m + LAZY2) mr = fmaxf(m, mt);
-        const float cf = (m == NEG_INF) ? 1.f : exp2f(m - mr);
-        if (__any(cf != 1.f)) {
+        half8 pa[RB][2];
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+            // scale (log2 units); the causal / start mask only where this tile crosses a row's window
+            if (__all(k0 >= start && k0 + 32 <= vis[b])) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) Scur[b][i] *= scale2;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int key = k0 + 8 * h + i + (i >= 8 ? 8 : 0);
+                    Scur[b][i] = (key < vis[b] && key >= start) ? Scur[b][i] * scale2 : NEG_INF;
+                }
+            }
+            float mt = Scur[b][0];
+#pragma unroll
+            for (int i = 1; i < 16; i++) mt = fmaxf(mt, Scur[b][i]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            float mr = m[b];
+            if (m[b] == NEG_INF || mt > m[b] + LAZY2) mr = fmaxf(m[b], mt);
+            const float cf = (m[b] == NEG_INF) ? 1.f : fast_exp2(m[b] - mr);
+            if (__any(cf != 1.f)) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float f = __shfl(cf, 8 * (i >> 2) + 4 * h + (i & 3));
+#pragma unroll
+                    for (int nb = 0; nb < 8; nb++) O[b][nb][i] *= f;
+                }
+            }
+            m[b] = mr;
+            // P = 2^(s - m): masked scores are -inf and give 0 (the reference is 0 while a row has seen no key);
+            // the row sum takes the f32 P, as attn_fa_mx does, the P.V operand its f16 rounding
+            const float base = mr == NEG_INF ? 0.f : mr;
+            float ls = 0.f;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float f = __shfl(cf, 8 * (i >> 2) + 4 * h + (i & 3));
-#pragma unroll
-                for (int nb = 0; nb < 8; nb++) O[nb][i] *= f;
+                const float p = fast_exp2(Scur[b][i] - base);
+                ls += p;
+                pa[b][i >> 3][i & 7] = (_Float16)p;
             }
+            lsum[b] = lsum[b] * cf + ls;
         }
-        lsum *= cf;
-        m = mr;
-        half8 pa[2];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const _Float16 ph = (_Float16)(S[i] > NEG_INF ? exp2f(S[i] - mr) : 0.f);
-            lsum += (float)ph;
-            pa[i >> 3][i & 7] = ph;
-        }
-        const bool tail = k0 + 32 > kend;  // V rows past the written length may hold anything: keep 0 * V finite
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
             for (int nb = 0; nb < 8; nb++) {
-                half8 vb = *(const half8*)(Vs + (2 * s2 + h) * 4096 + (32 * nb + r) * 16);
-                if (tail) {
+                const half8 vb = *(const half8*)(Vs + (2 * s2 + h) * 4096 + (32 * nb + r) * 16);
 #pragma unroll
-                    for (int jj = 0; jj < 8; jj++)
-                        if (k0 + 16 * s2 + 8 * h + jj >= kend) vb[jj] = (_Float16)0.f;
-                }
-                O[nb] = mfma32(pa[s2], vb, O[nb]);
+                for (int b = 0; b < RB; b++) O[b][nb] = mfma32(pa[b][s2], vb, O[b][nb]);
             }
     }
-    lsum += __shfl_xor(lsum, 32);
 
     // partials of this wave's rows of present tokens: row index t*8 + head of the kv head, rows per kv head = 8T
     const size_t rpk = (size_t)T * GQA;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int ri = 8 * (i >> 2) + 4 * h + (i & 3);
-        if (t0 + (ri >> 3) < T) {
-            float* p = part + ((kvh * rpk + (size_t)t0 * GQA + ri) * nch + sp) * PART + PACC + r;
+    for (int b = 0; b < RB; b++) {
+        lsum[b] += __shfl_xor(lsum[b], 32);
+        const int tb = t0 + 4 * b;
 #pragma unroll
-            for (int nb = 0; nb < 8; nb++) p[32 * nb] = O[nb][i];
+        for (int i = 0; i < 16; i++) {
+            const int ri = 8 * (i >> 2) + 4 * h + (i & 3);
+            if (tb + (ri >> 3) < T) {
+                float* p = part + ((kvh * rpk + (size_t)tb * GQA + ri) * nch + sp) * PART + PACC + r;
+#pragma unroll
+                for (int nb = 0; nb < 8; nb++) p[32 * nb] = O[b][nb][i];
+            }
         }
-    }
-    if (h == 0 && tr < T) {
-        float* p = part + ((kvh * rpk + (size_t)t0 * GQA + r) * nch + sp) * PART;
-        p[0] = m;
-        p[1] = lsum;
+        if (h == 0 && tb + (r >> 3) < T) {
+            float* p = part + ((kvh * rpk + (size_t)tb * GQA + r) * nch + sp) * PART;
+            p[0] = m[b];
+            p[1] = lsum[b];
+        }
     }
 }
 
@@ -176,8 +215,8 @@ hipError_t launch_prefill(const Geom& g, const void* base, int layer, const floa
     const void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
     const void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
     dim3 grid((T + PT - 1) / PT, p.nch, KVH);
-    return launch(prefill_f16, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.ch, p.nch,
-                  ws);
+    return launch(prefill_f16, grid, dim3(NW * 64), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.ch,
+                  p.nch, ws);
 }
 
 }  // namespace mkv

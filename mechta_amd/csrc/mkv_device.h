@@ -14,6 +14,10 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LAZY2 = 8.0f * LOG2E;  // DM_LAZY = 8 (dmx.rs:124) in log2 units
 constexpr float NEG_INF = -__builtin_huge_valf();
 
+// 2^x with the hardware's v_exp_f32 (no denormal scaffolding: results below 2^-126 flush to 0, far below the
+// smallest f16 P of 2^-24).
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ inline f32x16 mfma32(half8 a, half8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
