@@ -38,7 +38,7 @@ struct StageRegs {
 
 __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane, _Float16* __restrict__ vplane,
                                                   size_t plane_elems, const float* __restrict__ q, int ntok, int n,
-                                                  int start, float scale2, int ch, int nch, int c0,
+                                                  int start, float scale2, int span, int nch, int c0,
                                                   float* __restrict__ part, const float* __restrict__ akn,
                                                   const float* __restrict__ av, const float* __restrict__ atab,
                                                   int apos, int antok) {
@@ -46,18 +46,18 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     const int lane = tid & 63, w = tid >> 6;
     const int h = lane >> 5, r = lane & 31, l16 = lane & 15, g4 = lane >> 4;
     const int kend = n + ntok - 1;
-    const int cs = c * ch, ce = min(cs + ch, kend);
+    const int cs = chunk_lo(c, span, nch), ce = c + 1 < nch ? chunk_lo(c + 1, span, nch) : kend;
     _Float16* K = kplane + (size_t)kvh * plane_elems;
     _Float16* V = vplane + (size_t)kvh * plane_elems;
 
-    __shared__ float ss[2][ROWS][KPS + 1];  // partial S of the two dim halves, [row][key]
+    __shared__ __attribute__((aligned(16))) float ss[2][ROWS][KPS + 4];  // partial S of the two dim halves [row][key]
     __shared__ __attribute__((aligned(16))) _Float16 ps[ROWS][PS_STRIDE];
     __shared__ __attribute__((aligned(16))) float cfs[ROWS];
 
     // Fused append (mkv_append_decode): the work-group whose chunk holds new rows writes this kv head's K and V of
     // those rows (the same arithmetic as append_kernel) and makes them visible before any stage is loaded.
     {
-        const int p0 = max(apos, cs), p1 = min(apos + antok, cs + ch);
+        const int p0 = max(apos, cs), p1 = min(apos + antok, ce);
         if (p0 < p1) {
             unsigned short* Ku = (unsigned short*)K;
             unsigned short* Vu = (unsigned short*)V;
@@ -141,23 +141,27 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
         lds_barrier();
 
         // online softmax with the lazy reference max of attn_dmx (dmx.rs:72-86), log2 units
-        float sv[4], mt = NEG_INF;
+        const float4 x0 = *(const float4*)&ss[0][srow][4 * sq];
+        const float4 x1 = *(const float4*)&ss[1][srow][4 * sq];
+        float sv[4] = {(x0.x + x1.x) * scale2, (x0.y + x1.y) * scale2, (x0.z + x1.z) * scale2, (x0.w + x1.w) * scale2};
+        if (!(k0 >= start && k0 + KPS <= min(n, ce))) {  // the stage crosses a row's window or the chunk end
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int key = k0 + 4 * sq + i;
-            const float x = (ss[0][srow][4 * sq + i] + ss[1][srow][4 * sq + i]) * scale2;
-            sv[i] = (key < vis && key >= start && key < ce) ? x : NEG_INF;  // a stage may reach into the next chunk
-            mt = fmaxf(mt, sv[i]);
+            for (int i = 0; i < 4; i++) {
+                const int key = k0 + 4 * sq + i;
+                if (!(key < vis && key >= start && key < ce)) sv[i] = NEG_INF;
+            }
         }
+        float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         mt = reduce16(mt, [](float a, float b) { return fmaxf(a, b); });
         float mr = m_run;
         if (m_run == NEG_INF || mt > m_run + LAZY2) mr = fmaxf(m_run, mt);
-        const float cf = m_run == NEG_INF ? 1.f : exp2f(m_run - mr);
+        const float cf = m_run == NEG_INF ? 1.f : fast_exp2(m_run - mr);
+        const float base = mr == NEG_INF ? 0.f : mr;  // masked scores are -inf: 2^-inf = 0
         float psum = 0.f;
         _Float16 p4[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            p4[i] = (_Float16)(sv[i] > NEG_INF ? exp2f(sv[i] - mr) : 0.f);
+            p4[i] = (_Float16)fast_exp2(sv[i] - base);
             psum += (float)p4[i];
         }
         *(uint2*)&ps[srow][4 * sq] = *(const uint2*)p4;
@@ -219,11 +223,11 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
 // f32 store: VALU flash decode, 32-key tiles staged in LDS; thread (row, 4 keys) for S, thread = dim for P.V.
 __global__ void __launch_bounds__(256) decode_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
                                                   size_t plane_elems, const float* __restrict__ q, int ntok, int n,
-                                                  int start, float scale2, int ch, int nch, int c0,
+                                                  int start, float scale2, int span, int nch, int c0,
                                                   float* __restrict__ part) {
     const int kvh = blockIdx.y, c = c0 + blockIdx.x, tid = threadIdx.x;
     const int kend = n + ntok - 1;
-    const int cs = c * ch, ce = min(cs + ch, kend);
+    const int cs = chunk_lo(c, span, nch), ce = c + 1 < nch ? chunk_lo(c + 1, span, nch) : kend;
     const float* K = kplane + (size_t)kvh * plane_elems;
     const float* V = vplane + (size_t)kvh * plane_elems;
     const int nrows = 8 * ntok;
@@ -318,12 +322,13 @@ __global__ void __launch_bounds__(256) decode_f32(const float* __restrict__ kpla
 // 16 dim lanes (4 dims each), so every chunk's 64 dims are one coalesced 256-byte read and all chunks are in flight at
 // once; the 16 chunk lanes are then summed in LDS.
 __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ part, int rpk, int n, int start,
-                                                      int ch, int nch, const float* __restrict__ gate,
+                                                      int span, int nch, const float* __restrict__ gate,
                                                       float* __restrict__ out) {
     const int t = blockIdx.x / QH, head = blockIdx.x % QH, dq = blockIdx.y, tid = threadIdx.x;
     const int kvh = head / GQA, row = t * GQA + head % GQA;
     const float* p = part + ((size_t)kvh * rpk + row) * nch * PART;
-    const int c0 = start / ch, c1 = (n + t + ch - 1) / ch;  // chunks holding a key of [start, n + t)
+    int c0, c1;  // chunks holding a key of [start, n + t)
+    chunk_range(start, n + t, span, nch, c0, c1);
     __shared__ float red[4];
     __shared__ float4 acc4[16][16];
     __shared__ float redl[16];
@@ -387,12 +392,13 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
 
 // Merge for few chunks (prefill splits): work-group = (token, head), thread = dim; all chunks of the row are loaded
 // in one round trip.
-__global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part, int rpk, int n, int start, int ch,
+__global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part, int rpk, int n, int start, int span,
                                                  int nch, const float* __restrict__ gate, float* __restrict__ out) {
     const int t = blockIdx.x / QH, head = blockIdx.x % QH, d = threadIdx.x;
     const int kvh = head / GQA, row = t * GQA + head % GQA;
     const float* p = part + ((size_t)kvh * rpk + row) * nch * PART;
-    const int c0 = start / ch, c1 = (n + t + ch - 1) / ch;
+    int c0, c1;  // chunks holding a key of [start, n + t)
+    chunk_range(start, n + t, span, nch, c0, c1);
     float mj[MERGE_FEW], lj[MERGE_FEW], aj[MERGE_FEW];
     float M = NEG_INF;
 #pragma unroll
@@ -427,10 +433,17 @@ __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part,
 
 DecodePlan decode_plan(int n, int ntok, int start) {
     const int kend = n + ntok - 1;
-    int ch = (kend + 127) / 128;  // about 128 chunks per kv head: 256 work-groups for 256 CUs
-    ch = (ch + KBLK - 1) / KBLK * KBLK;  // whole K blocks; a stage may reach 32 keys past the chunk (store slack)
-    if (ch < 128) ch = 128;
-    return DecodePlan{ch, (kend + ch - 1) / ch, start / ch};
+    // chunks of at least 128 positions, at most 124 per kv head: 248 work-groups on the 256 CUs, one each. (Measured
+    // at 64K positions: 124 chunks of 512 or 544 positions beat 128, 120 and 112 -- the work-group with the most
+    // 64-position stages sets the time.)
+    int nch = kend / 128;
+    nch = nch < 1 ? 1 : nch > 124 ? 124 : nch;
+    // boundaries planned over kend + half a chunk: the last chunk, whose work-group also writes the appended rows
+    // (mkv_append_decode), is about half as long as the others and does not finish last
+    const int span = kend + kend / (2 * nch);
+    int c0, c1;
+    chunk_range(start, kend, span, nch, c0, c1);
+    return DecodePlan{span, nch, c0};
 }
 
 hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float* q, int ntok, int n, int start,
@@ -443,24 +456,24 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
     const float scale2 = scale * LOG2E;
     dim3 grid(p.nch - p.c0, KVH);
     if (g.fmt == 0)
-        return launch(decode_f16, grid, dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.ch, p.nch,
+        return launch(decode_f16, grid, dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.span, p.nch,
                       p.c0, ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
     if (fa.ntok) return hipErrorNotSupported;
-    return launch(decode_f32, grid, dim3(256), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.ch, p.nch, p.c0,
+    return launch(decode_f32, grid, dim3(256), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.span, p.nch, p.c0,
                   ws.part);
 }
 
-hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int ch, int nch, const float* gate,
+hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,
                         float* out, const Launch& L) {
-    if (nch - start / ch > 16 * MERGE_J) return hipErrorInvalidValue;
-    if (nch - start / ch <= MERGE_FEW)
-        return launch(merge_few, dim3(ntok * QH), dim3(256), L, part, rpk, n, start, ch, nch, gate, out);
-    return launch(decode_combine, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, ch, nch, gate, out);
+    if (nch > 16 * MERGE_J) return hipErrorInvalidValue;
+    if (nch <= MERGE_FEW)
+        return launch(merge_few, dim3(ntok * QH), dim3(256), L, part, rpk, n, start, span, nch, gate, out);
+    return launch(decode_combine, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, span, nch, gate, out);
 }
 
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
                                float* out, const Launch& L) {
-    return launch_merge(ws.part, ROWS, ntok, n, start, p.ch, p.nch, gate, out, L);
+    return launch_merge(ws.part, ROWS, ntok, n, start, p.span, p.nch, gate, out, L);
 }
 
 }  // namespace mkv

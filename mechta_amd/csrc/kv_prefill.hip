@@ -35,14 +35,14 @@ __device__ inline void wait_tiles(int later) {  // at most `later` tiles (4 dire
 __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restrict__ kplane,
                                                    const _Float16* __restrict__ vplane, size_t plane_elems,
                                                    const float* __restrict__ q, int T, int n, int start, float scale2,
-                                                   int ch, int nch, float* __restrict__ part) {
+                                                   int span, int nch, float* __restrict__ part) {
     const int rb = blockIdx.x, sp = blockIdx.y, kvh = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int h = lane >> 5, r = lane & 31;
     const int t0 = rb * PT + 4 * RB * w;     // this wave's first token; row block b holds tokens t0 + 4b .. +3
     const int tlast = min(T - 1, rb * PT + PT - 1);
     const int kend = n + T - 1;              // positions written for this block
-    const int cs = sp * ch, ce = min(cs + ch, n + tlast);
+    const int cs = chunk_lo(sp, span, nch), ce = min(sp + 1 < nch ? chunk_lo(sp + 1, span, nch) : span, n + tlast);
     if (cs >= ce) return;                    // no key of this split is seen by these tokens: never merged
     const _Float16* K = kplane + (size_t)kvh * plane_elems;
     const _Float16* V = vplane + (size_t)kvh * plane_elems;
@@ -198,12 +198,12 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
 
 PrefillPlan prefill_plan(int T, int n) {
     const int kend = n + T - 1;
-    const int blocks = 2 * ((T + PT - 1) / PT);       // work-groups per split
-    int nch = 256 / blocks;                           // about one work-group per CU
+    const int blocks = 2 * ((T + PT - 1) / PT);  // work-groups per split
+    int nch = 256 / blocks;                      // about one work-group per CU
+    const int most = kend / 64;                  // splits of at least 64 positions
+    nch = nch > most ? most : nch;
     nch = nch < 1 ? 1 : nch > 16 ? 16 : nch;
-    int ch = (kend + nch - 1) / nch;
-    ch = (ch + KBLK - 1) / KBLK * KBLK;               // whole 32-key tiles
-    return PrefillPlan{ch, (kend + ch - 1) / ch};
+    return PrefillPlan{kend, nch};
 }
 
 size_t prefill_ws_floats(int T, int nch) { return (size_t)KVH * T * GQA * nch * PART; }
@@ -215,7 +215,7 @@ hipError_t launch_prefill(const Geom& g, const void* base, int layer, const floa
     const void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
     const void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
     dim3 grid((T + PT - 1) / PT, p.nch, KVH);
-    return launch(prefill_f16, grid, dim3(NW * 64), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.ch,
+    return launch(prefill_f16, grid, dim3(NW * 64), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
                   p.nch, ws);
 }
 

@@ -310,7 +310,7 @@ int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, fl
         });
         if (e == hipSuccess)
             e = traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {
-                return launch_merge(h->pws, T * GQA, T, n, start, p.ch, p.nch, gate, out, L);
+                return launch_merge(h->pws, T * GQA, T, n, start, p.span, p.nch, gate, out, L);
             });
     } else {
         // f32 store: exact f32 attention of the decode kernel, 4 tokens per launch (each token's causal window)

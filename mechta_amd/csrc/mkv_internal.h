@@ -54,6 +54,21 @@ __device__ inline float rope_dim(const float* __restrict__ a, const float* __res
     return a[d];
 }
 
+// Split-K chunks: chunk c (of nch) starts at chunk_lo(c) = c * span / nch rounded down to a whole 32-position K block;
+// the last chunk ends where the keys end (span may exceed them: the last chunk is then shorter than the others).
+__host__ __device__ inline int chunk_lo(int c, int span, int nch) {
+    return (int)((long long)c * span / nch / KBLK * KBLK);
+}
+// Chunks [c0, c1) are the ones holding a position of [lo, hi) (lo < hi <= the keys' end).
+__host__ __device__ inline void chunk_range(int lo, int hi, int span, int nch, int& c0, int& c1) {
+    c0 = (int)((long long)lo * nch / span);  // estimates, then exact by the boundaries
+    while (c0 > 0 && chunk_lo(c0, span, nch) > lo) c0--;
+    while (c0 + 1 < nch && chunk_lo(c0 + 1, span, nch) <= lo) c0++;
+    c1 = (int)((long long)hi * nch / span);
+    while (c1 > 0 && chunk_lo(c1, span, nch) >= hi) c1--;
+    while (c1 < nch && chunk_lo(c1, span, nch) < hi) c1++;
+}
+
 // Geometry of one store, passed by value to launchers.
 struct Geom {
     int layers, ctx, fmt;  // fmt: 0 = f16, 1 = f32
@@ -106,7 +121,7 @@ hipError_t launch_write_rows(const Geom& g, void* base, int layer, int which, in
                              const Launch& L);
 // Split-K pass and merge of the decode (two kernels).
 struct DecodePlan {
-    int ch, nch, c0;
+    int span, nch, c0;  // chunks of [0, span); chunks below c0 end before `start`
 };
 DecodePlan decode_plan(int n, int ntok, int start);
 hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float* q, int ntok, int n, int start,
@@ -115,12 +130,12 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
                                float* out, const Launch& L);
 // Merge of split-K partials laid out [kvh][row < rpk][chunk < nch][PART], row = token*8 + head of the kv head:
-// out[t][head] for t < ntok over the chunks of ch positions holding a key of [start, n + t), optional output gate.
-hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int ch, int nch, const float* gate,
+// out[t][head] for t < ntok over the chunks (chunk_lo of span, nch) holding a key of [start, n + t), optional gate.
+hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,
                         float* out, const Launch& L);
 // Prefill (f16 store): split-K pass into the partials ws, then launch_merge with the returned plan.
 struct PrefillPlan {
-    int ch, nch;  // positions per split, splits
+    int span, nch;  // splits of [0, span) as chunk_lo
 };
 PrefillPlan prefill_plan(int T, int n);
 size_t prefill_ws_floats(int T, int nch);
