@@ -34,6 +34,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy kernel (reference for HBM counter scaling)")
     return ap.parse_args()
 
 
@@ -220,6 +222,14 @@ def main():
             res["roofline_prefill"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_MFMA_PEAK_TFLOPS,
                                        "unit": "TFLOP/s", "frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
                                        "kernel": "prefill_f16"}
+    if args.calib_copy:
+        # plain elementwise copy of a known size: its FETCH_SIZE / WRITE_SIZE counters give the scale from counter
+        # units to bytes for the KV kernels' counters in the same run
+        src = torch.ones(64 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.add(src, 0.0, out=dst)
+        torch.cuda.synchronize()
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(dec, args.cpu_seconds)
     print(json.dumps(res), flush=True)

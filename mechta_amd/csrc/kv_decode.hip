@@ -25,8 +25,18 @@
 namespace mkv {
 namespace {
 
-constexpr int KPS = 64;                        // keys per stage of the decode ring
+constexpr int KPS = KPS_F16;                   // keys per stage of the decode ring
+#ifndef MKV_DEC_WG
+#define MKV_DEC_WG 124
+#endif
+constexpr int DEC_WG = MKV_DEC_WG;             // most work-groups per kv head (2 x 124 on the 256 CUs)
+#ifndef MKV_DEC_NSET
+#define MKV_DEC_NSET 3
+#endif
+constexpr int DEC_NSET = MKV_DEC_NSET;         // register sets of the decode pipeline
 constexpr int PS_STRIDE = KPS + 8;             // halves per P row in LDS (conflict-free 16-byte reads)
+constexpr int QS_STRIDE = HD + 8;              // halves per Q row in LDS
+constexpr int NEWMAX = 4;                      // appended rows per call
 constexpr int MERGE_FEW = 16;  // chunks of the one-lane-per-dim merge
 constexpr int MERGE_J = 9;  // chunks per merge lane: 16 lanes x 9 >= the at most 130 chunks of decode_plan
 
@@ -36,48 +46,43 @@ struct StageRegs {
     half8 v[4];
 };
 
+// NSET register sets of stage operands (2 to 4): NSET - 1 stages in flight ahead of the one computed.
+template <int NSET>
 __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane, _Float16* __restrict__ vplane,
                                                   size_t plane_elems, const float* __restrict__ q, int ntok, int n,
-                                                  int start, float scale2, int span, int nch, int c0,
+                                                  int start, float scale2, int s0, int nu,
                                                   float* __restrict__ part, const float* __restrict__ akn,
                                                   const float* __restrict__ av, const float* __restrict__ atab,
                                                   int apos, int antok) {
-    const int kvh = blockIdx.y, c = c0 + blockIdx.x, tid = threadIdx.x;
+    const int kvh = blockIdx.y, c = blockIdx.x, nch = gridDim.x, tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int h = lane >> 5, r = lane & 31, l16 = lane & 15, g4 = lane >> 4;
     const int kend = n + ntok - 1;
-    const int cs = chunk_lo(c, span, nch), ce = c + 1 < nch ? chunk_lo(c + 1, span, nch) : kend;
+    // Stages are dealt so that the partial round comes first: with R = nu / nch and r = nu % nch, stage u >= r goes
+    // to work-group (u - r) % nch, so every work-group takes R of them and the last stage (the one holding appended
+    // rows) goes to work-group nch - 1. The first r stages are the partial round: when 2r <= nch they are split into
+    // 2r half stages of 32 positions for work-groups 0 .. 2r - 1 (the busiest work-group then has R + 1/2 stages),
+    // else stage u < r goes to work-group u.
+    const int rr = nu % nch;
+    const bool halves = 2 * rr <= nch;
+    const int ex = c < (halves ? 2 * rr : rr);  // this work-group's stage 0 is from the partial round
+    auto kbase = [&](int j) {
+        return ex && j == 0 ? s0 + c * (halves ? KPS / 2 : KPS) : s0 + (rr + c + (j - ex) * nch) * KPS;
+    };
+    auto klen = [&](int j) { return ex && j == 0 && halves ? KPS / 2 : KPS; };
+    auto owner = [&](int u) { return (u - rr) % nch; };  // of a stage u >= r (every stage that can hold new rows)
     _Float16* K = kplane + (size_t)kvh * plane_elems;
     _Float16* V = vplane + (size_t)kvh * plane_elems;
 
-    __shared__ __attribute__((aligned(16))) float ss[2][ROWS][KPS + 4];  // partial S of the two dim halves [row][key]
-    __shared__ __attribute__((aligned(16))) _Float16 ps[ROWS][PS_STRIDE];
-    __shared__ __attribute__((aligned(16))) float cfs[ROWS];
-
-    // Fused append (mkv_append_decode): the work-group whose chunk holds new rows writes this kv head's K and V of
-    // those rows (the same arithmetic as append_kernel) and makes them visible before any stage is loaded.
-    {
-        const int p0 = max(apos, cs), p1 = min(apos + antok, ce);
-        if (p0 < p1) {
-            unsigned short* Ku = (unsigned short*)K;
-            unsigned short* Vu = (unsigned short*)V;
-            for (int it = tid; it < (p1 - p0) * 32; it += 512) {
-                const int p = p0 + (it >> 5), d0 = (it & 31) * 8, t = p - apos;
-                const float* a = akn + ((size_t)t * KVH + kvh) * HD;
-                const float* tb = atab + (size_t)t * 64;
-                u16x8 w8;
-#pragma unroll
-                for (int j = 0; j < 8; j++) w8[j] = f2h(rope_dim(a, tb, d0 + j));
-                *(u16x8*)(Ku + k_off(p, d0)) = w8;
-            }
-            for (int it = tid; it < (p1 - p0) * HD; it += 512) {
-                const int p = p0 + it / HD, d = it % HD;
-                Vu[v_off(p, d)] = f2h(av[(size_t)(p - apos) * (KVH * HD) + kvh * HD + d]);
-            }
-            __threadfence();
-            __syncthreads();
-        }
-    }
+    // double-buffered by stage parity: partial S of the two dim halves [row][key], P [row][key], rescale factors
+    __shared__ __attribute__((aligned(16))) float ss[2][2][ROWS][KPS + 4];
+    __shared__ __attribute__((aligned(16))) _Float16 ps[2][ROWS][PS_STRIDE];
+    __shared__ __attribute__((aligned(16))) float cfs[2][ROWS];
+    __shared__ __attribute__((aligned(16))) _Float16 qs[ROWS][QS_STRIDE];
+    // fused append: the new rows' inputs (K normed, V, RoPE table) and their f16 store values
+    __shared__ __attribute__((aligned(16))) float ain[2 * NEWMAX * HD + NEWMAX * 64];
+    __shared__ __attribute__((aligned(16))) _Float16 newk[NEWMAX][HD];
+    __shared__ __attribute__((aligned(16))) _Float16 newv[NEWMAX][HD];
 
     // Roles of wave w in a 64-key stage:
     //   S: keys 16kq .. 16kq + 15 (kq = w % 4) times dims 128dh .. 128dh + 127 (dh = w / 4), both 16-row halves,
@@ -86,69 +91,136 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     //   P.V: dims 32w .. 32w + 31 of all 32 rows, v_mfma_f32_32x32x16_f16, B = V (lane: dim 32w + lane%32,
     //      8 keys 16s2 + 8(lane/32) .. of group 2s2 + lane/32).
     const int kq = w & 3, dh = w >> 2;
-    const int nst = (ce - cs + KPS - 1) / KPS;
+    const int nst = nu / nch + ex;
     const int kkey = 16 * kq + l16;  // S-role key inside the stage
+    // Buffer loads through a resource that starts at the stage's first key and ends at the keys' end (rounded up to
+    // the 32-key K block and the 8-key V group): loads past the keys, and every load of a stage past this
+    // work-group's last, are out of range and move no bytes. The per-lane offsets inside a stage are loop constants.
+    const int ceK = (kend + KBLK - 1) / KBLK * KBLK, ceV = (kend + VGRP - 1) / VGRP * VGRP;
+    const unsigned kofs = (unsigned)(((kkey / KBLK) * (KBLK * HD) + (kkey % KBLK) * 8 + (16 * dh + g4) * (KBLK * 8)) * 2);
+    const unsigned vofs = (unsigned)((h * (VGRP * HD) + (32 * w + r) * VGRP) * 2);
     auto load = [&](int j, StageRegs& R) {
-        const int k0 = cs + j * KPS;
-        const _Float16* kb = K + (size_t)((k0 + kkey) / KBLK) * (KBLK * HD) + ((k0 + kkey) % KBLK) * 8;
+        const int k0 = kbase(j);  // a multiple of 64: the stage starts a K block and a V group
+        const int len = klen(j);
+        const rsrc_t kr = plane_rsrc(K + (size_t)k0 * HD, (unsigned)(max(min(ceK - k0, len), 0) * (HD * 2)));
+        const rsrc_t vr = plane_rsrc(V + (size_t)k0 * HD, (unsigned)(max(min(ceV - k0, len), 0) * (HD * 2)));
 #pragma unroll
-        for (int s = 0; s < 4; s++) R.k[s] = *(const half8*)(kb + (16 * dh + 4 * s + g4) * (KBLK * 8));
-        const _Float16* vb = V + (size_t)(k0 / VGRP + h) * (VGRP * HD) + (32 * w + r) * VGRP;
+        for (int s = 0; s < 4; s++) R.k[s] = bload16(kr, kofs + s * (4 * KBLK * 8 * 2));
 #pragma unroll
-        for (int s2 = 0; s2 < 4; s2++) R.v[s2] = *(const half8*)(vb + s2 * 2 * (VGRP * HD));
+        for (int s2 = 0; s2 < 4; s2++) R.v[s2] = bload16(vr, vofs + s2 * (2 * VGRP * HD * 2));
     };
-    StageRegs RA, RB, RC;
-    if (nst > 0) load(0, RA);
-    if (nst > 1) load(1, RB);
-
-    // Q (rounded to f16 as q_dmx) as B operand, straight into registers: rows 16hb + lane%16, dims
-    // 128dh + 32s + 8(lane/16) .. +7; rows of absent tokens are zero
-    half8 qb[2][4];
+    // Fused append (mkv_append_decode). The new rows [apf, apl) of the stages this work-group owns (at most two
+    // stages hold new rows) are computed into LDS (the same arithmetic as append_kernel) and patched into the K and V
+    // registers of the stage that holds them, so no load waits for their stores; they are stored to the planes
+    // after the loop, for the launches that follow. Their inputs come into LDS by direct loads issued before Q's and
+    // the stages', and a wait for all but those later loads makes them available while the stages stream.
+    const int ua = antok > 0 ? (apos - s0) / KPS : 0, ub = antok > 0 ? (apos + antok - 1 - s0) / KPS : -1;
+    int apf = 0, apl = 0;
+    for (int u = ua; u <= ub; u++)
+        if (owner(u) == c) {
+            const int lo = max(apos, s0 + u * KPS), hi = min(apos + antok, s0 + (u + 1) * KPS);
+            apf = apl == 0 ? lo : apf;
+            apl = hi;
+        }
+    const int nr = apl - apf;  // 0 .. 4 new rows here, contiguous
+    float* const aink = ain;
+    float* const ainv = ain + NEWMAX * HD;
+    float* const aint = ain + 2 * NEWMAX * HD;
+    if (nr > 0) {
+        const int t0 = apf - apos;
+        for (int i = w; i < 2 * nr + 1; i += 8) {  // 1 KB per direct load: K rows, V rows, then the table rows
+            if (i < nr)
+                dma16(akn + ((size_t)(t0 + i) * KVH + kvh) * HD + 4 * lane, aink + i * HD);
+            else if (i < 2 * nr)
+                dma16(av + (size_t)(t0 + i - nr) * (KVH * HD) + kvh * HD + 4 * lane, ainv + (i - nr) * HD);
+            else if (lane < 16 * nr)
+                dma16(atab + (size_t)t0 * 64 + 4 * lane, aint);
+        }
+    }
+    float4 xq[2][2];  // Q loads before the stages': loads complete in order, so the first stage's wait covers them
 #pragma unroll
-    for (int hb = 0; hb < 2; hb++) {
-        const int row = 16 * hb + l16, tq = row >> 3;
-        const float* qr = q + ((size_t)min(tq, ntok - 1) * QH + kvh * GQA + (row & 7)) * HD + 128 * dh + 8 * g4;
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            float4 x0 = *(const float4*)(qr + 32 * s), x1 = *(const float4*)(qr + 32 * s + 4);
-            if (tq >= ntok) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
-            qb[hb][s] = half8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
-                              (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
+    for (int i = 0; i < 2; i++) {
+        const int idx = tid + 512 * i, row = idx >> 5, d8 = (idx & 31) * 8, tq = row >> 3;
+        const float* qr = q + ((size_t)min(tq, ntok - 1) * QH + kvh * GQA + (row & 7)) * HD + d8;
+        xq[i][0] = *(const float4*)qr;
+        xq[i][1] = *(const float4*)(qr + 4);
+    }
+    // three stages in flight from the start; loads of stages past this work-group's last are out of range and move
+    // no bytes, so no load is behind a branch (a branch around loads makes the compiler's wait counts pessimistic)
+    StageRegs R0, R1, R2, R3;
+    load(0, R0);
+    if constexpr (NSET > 2) load(1, R1);
+    if constexpr (NSET > 3) load(2, R2);
+    if (nr > 0) {
+        // the direct loads precede the 4 Q and the stage loads; then every wave's LDS data is in
+        static_assert(NSET >= 2 && NSET <= 4, "wait counts below");
+        if constexpr (NSET == 2) asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
+        if constexpr (NSET == 3) asm volatile("s_waitcnt vmcnt(20)\n\ts_barrier" ::: "memory");
+        if constexpr (NSET == 4) asm volatile("s_waitcnt vmcnt(28)\n\ts_barrier" ::: "memory");
+        for (int it = tid; it < nr * HD; it += 512) {
+            const int i = it / HD, d = it % HD;
+            newk[i][d] = __builtin_bit_cast(_Float16, f2h(rope_dim(aink + i * HD, aint + i * 64, d)));
+            newv[i][d] = __builtin_bit_cast(_Float16, f2h(ainv[i * HD + d]));
         }
     }
 
+    // Q rounded to f16 (as q_dmx) into LDS, [row][dim]; rows of absent tokens are zero
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int idx = tid + 512 * i, row = idx >> 5, d8 = (idx & 31) * 8, tq = row >> 3;
+        float4 x0 = xq[i][0], x1 = xq[i][1];
+        if (tq >= ntok) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+        *(half8*)&qs[row][d8] = half8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
+                                      (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
+    }
+    lds_barrier();
+
     // softmax role: thread (srow, sq) owns keys 4sq .. 4sq+3 of row srow; the row's 16 threads keep identical m, l
     const int srow = tid >> 4, sq = tid & 15;
-    const int vis = n + (srow >> 3);  // row srow sees keys < vis
+    const int vis = min(n + (srow >> 3), kend);  // row srow sees keys < vis (rows of absent tokens: < kend)
     float m_run = NEG_INF, l_run = 0.f;
     f32x16 O = f32x16{};
 
-    auto stage = [&](int j, StageRegs& R, StageRegs& Rnext2, auto steady) {
-        // two stages in flight while this one is computed (unconditional in the steady loop: branches around loads
-        // make the compiler's wait counts pessimistic)
-        if (decltype(steady)::value || j + 2 < nst) load(j + 2, Rnext2);
-        const int k0 = cs + j * KPS;
+    // S partial of this wave's 16 keys x 32 rows over its 128 dims, into ss[buf][dh]
+    auto s_part = [&](int j, const StageRegs& R, int buf) {
+        half8 kk[4] = {R.k[0], R.k[1], R.k[2], R.k[3]};
+        const int k0 = kbase(j);
+        if (k0 < apl && k0 + KPS > apf) {  // the stage holds new rows: their K from LDS
+            const int key = k0 + kkey;
+            if (key >= apf && key < apl) {
+#pragma unroll
+                for (int s = 0; s < 4; s++) kk[s] = *(const half8*)&newk[key - apf][128 * dh + 32 * s + 8 * g4];
+            }
+        }
         f32x4 s4[2] = {f32x4{}, f32x4{}};
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            s4[0] = mfma16(R.k[s], qb[0][s], s4[0]);
-            s4[1] = mfma16(R.k[s], qb[1][s], s4[1]);
+            // B = Q^T: rows 16hb + lane%16, dims 128dh + 32s + 8(lane/16) .. +7
+            const half8 q0 = *(const half8*)&qs[l16][128 * dh + 32 * s + 8 * g4];
+            const half8 q1 = *(const half8*)&qs[16 + l16][128 * dh + 32 * s + 8 * g4];
+            s4[0] = mfma16(kk[s], q0, s4[0]);
+            s4[1] = mfma16(kk[s], q1, s4[1]);
         }
+        return [&, s4, buf]() {
 #pragma unroll
-        for (int hb = 0; hb < 2; hb++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) ss[dh][16 * hb + l16][16 * kq + 4 * g4 + i] = s4[hb][i];
-        lds_barrier();
+            for (int hb = 0; hb < 2; hb++)
+                *(f32x4*)&ss[buf][dh][16 * hb + l16][16 * kq + 4 * g4] = s4[hb];
+        };
+    };
 
-        // online softmax with the lazy reference max of attn_dmx (dmx.rs:72-86), log2 units
-        const float4 x0 = *(const float4*)&ss[0][srow][4 * sq];
-        const float4 x1 = *(const float4*)&ss[1][srow][4 * sq];
+    // online softmax of stage j with the lazy reference max of attn_dmx (dmx.rs:72-86), log2 units: reads ss[buf],
+    // writes P (f16) to ps[buf] and the rows' rescale factors to cfs[buf]
+    auto softmax = [&](int j, int buf) {
+        const int k0 = kbase(j);
+        const float4 x0 = *(const float4*)&ss[buf][0][srow][4 * sq];
+        const float4 x1 = *(const float4*)&ss[buf][1][srow][4 * sq];
         float sv[4] = {(x0.x + x1.x) * scale2, (x0.y + x1.y) * scale2, (x0.z + x1.z) * scale2, (x0.w + x1.w) * scale2};
-        if (!(k0 >= start && k0 + KPS <= min(n, ce))) {  // the stage crosses a row's window or the chunk end
+        const int kcap = k0 + klen(j);
+        if (!(k0 >= start && kcap <= n && kcap == k0 + KPS)) {  // the stage crosses a row's window or is a half
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int key = k0 + 4 * sq + i;
-                if (!(key < vis && key >= start && key < ce)) sv[i] = NEG_INF;
+                if (!(key < vis && key >= start && key < kcap)) sv[i] = NEG_INF;
             }
         }
         float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
@@ -157,54 +229,154 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
         if (m_run == NEG_INF || mt > m_run + LAZY2) mr = fmaxf(m_run, mt);
         const float cf = m_run == NEG_INF ? 1.f : fast_exp2(m_run - mr);
         const float base = mr == NEG_INF ? 0.f : mr;  // masked scores are -inf: 2^-inf = 0
-        float psum = 0.f;
-        _Float16 p4[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            p4[i] = (_Float16)fast_exp2(sv[i] - base);
-            psum += (float)p4[i];
-        }
-        *(uint2*)&ps[srow][4 * sq] = *(const uint2*)p4;
+        typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+        const half2v p01 = {(_Float16)fast_exp2(sv[0] - base), (_Float16)fast_exp2(sv[1] - base)};
+        const half2v p23 = {(_Float16)fast_exp2(sv[2] - base), (_Float16)fast_exp2(sv[3] - base)};
+        const half2v one2 = {(_Float16)1.f, (_Float16)1.f};
+        // l adds the f16-rounded P, summed in f32 (v_dot2_f32_f16 is exact for these products by 1)
+        float psum = __builtin_amdgcn_fdot2(p23, one2, __builtin_amdgcn_fdot2(p01, one2, 0.f, false), false);
+        *(uint2*)&ps[buf][srow][4 * sq] = uint2{__builtin_bit_cast(unsigned, p01), __builtin_bit_cast(unsigned, p23)};
         psum = reduce16(psum, [](float a, float b) { return a + b; });
         l_run = l_run * cf + psum;
         m_run = mr;
-        if (sq == 0) cfs[srow] = cf;
-        lds_barrier();
+        if (sq == 0) cfs[buf][srow] = cf;
+    };
 
-        if (__any(cfs[r] != 1.f)) {
+    // O (this wave's 32 dims of the 32 rows) = O * cf + P . V of stage j
+    auto pv = [&](int j, int buf, const StageRegs& R) {
+        const int k0 = kbase(j);
+        half8 pa[KPS / 16];
+#pragma unroll
+        for (int s2 = 0; s2 < KPS / 16; s2++) pa[s2] = *(const half8*)&ps[buf][r][16 * s2 + 8 * h];
+        if (__any(cfs[buf][r] != 1.f)) {
 #pragma unroll
             for (int a = 0; a < 4; a++) {
-                const float4 f = *(const float4*)&cfs[8 * a + 4 * h];
+                const float4 f = *(const float4*)&cfs[buf][8 * a + 4 * h];
                 O[4 * a] *= f.x;
                 O[4 * a + 1] *= f.y;
                 O[4 * a + 2] *= f.z;
                 O[4 * a + 3] *= f.w;
             }
         }
-        const bool tail = k0 + KPS > kend;  // V rows past the written length may hold anything: keep 0 * V finite
+        half8 vb[KPS / 16] = {R.v[0], R.v[1], R.v[2], R.v[3]};
+        if (k0 < apl && k0 + KPS > apf) {  // the stage holds new rows: their V from LDS
 #pragma unroll
-        for (int s2 = 0; s2 < KPS / 16; s2++) {
-            const half8 pa = *(const half8*)&ps[r][16 * s2 + 8 * h];
-            half8 vb = R.v[s2];
-            if (tail) {
+            for (int s2 = 0; s2 < KPS / 16; s2++) {
+                if (k0 + 16 * s2 >= apl || k0 + 16 * s2 + 16 <= apf) continue;  // no new row in these 16 keys
+                _Float16 x[8];  // all reads first (clamped rows), then the selects: no LDS round trip per key
 #pragma unroll
                 for (int jj = 0; jj < 8; jj++)
-                    if (k0 + 16 * s2 + 8 * h + jj >= kend) vb[jj] = (_Float16)0.f;
+                    x[jj] = newv[min(max(k0 + 16 * s2 + 8 * h + jj - apf, 0), nr - 1)][32 * w + r];
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) {
+                    const int key = k0 + 16 * s2 + 8 * h + jj;
+                    if (key >= apf && key < apl) vb[s2][jj] = x[jj];
+                }
             }
-            O = mfma32(pa, vb, O);
         }
+        if (k0 + KPS > kend) {  // V rows past the written length may hold anything: keep 0 * V finite
+#pragma unroll
+            for (int s2 = 0; s2 < KPS / 16; s2++)
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++)
+                    if (k0 + 16 * s2 + 8 * h + jj >= kend) vb[s2][jj] = (_Float16)0.f;
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < KPS / 16; s2++) O = mfma32(pa[s2], vb[s2], O);
     };
-    // register sets rotate with period 3: (this stage, stage + 2) = (A, C), (B, A), (C, B)
-    int j = 0;
-    for (; j + 5 <= nst; j += 3) {
-        stage(j, RA, RC, std::true_type{});
-        stage(j + 1, RB, RA, std::true_type{});
-        stage(j + 2, RC, RB, std::true_type{});
+
+    // Software pipeline, one barrier per stage. Iteration j: issue the loads of stage j + NSET - 1, the S MFMAs of
+    // stage j + 1 (they run while the VALU does the softmax of stage j, whose S the previous iteration left in LDS),
+    // store S of j + 1, barrier, then P.V of stage j. Buffers alternate by stage parity; a buffer is rewritten two
+    // stages after it was read, behind the barrier between. Register sets rotate with period NSET: stage j's V is in
+    // R[j % NSET], stage j + 1's K in R[(j + 1) % NSET], and stage j + NSET - 1 loads into R[(j - 1) % NSET].
+    auto iter = [&](int j, const StageRegs& Rj, const StageRegs& Rj1, StageRegs& Rjn, auto has_next) {
+        const int buf = j & 1;
+        load(j + NSET - 1, Rjn);
+        if constexpr (decltype(has_next)::value) {
+            auto store_s = s_part(j + 1, Rj1, buf ^ 1);
+            softmax(j, buf);
+            store_s();
+        } else {
+            softmax(j, buf);
+        }
+        lds_barrier();
+        pv(j, buf, Rj);
+    };
+    if (nst > 0) {
+        s_part(0, R0, 0)();
+        lds_barrier();
     }
-    if (j < nst) stage(j, RA, RC, std::false_type{});
-    if (j + 1 < nst) stage(j + 1, RB, RA, std::false_type{});
-    if (j + 2 < nst) stage(j + 2, RC, RB, std::false_type{});
-    if (j + 3 < nst) stage(j + 3, RA, RC, std::false_type{});
+    using T = std::true_type;
+    using F = std::false_type;
+    int j = 0;
+    if constexpr (NSET == 4) {
+        for (; j + 5 <= nst; j += 4) {
+            iter(j, R0, R1, R3, T{});
+            iter(j + 1, R1, R2, R0, T{});
+            iter(j + 2, R2, R3, R1, T{});
+            iter(j + 3, R3, R0, R2, T{});
+        }
+        const int rem = nst - j;  // the last 1 to 4 stages, straight-line
+        if (rem == 1) {
+            iter(j, R0, R1, R3, F{});
+        } else if (rem == 2) {
+            iter(j, R0, R1, R3, T{});
+            iter(j + 1, R1, R2, R0, F{});
+        } else if (rem == 3) {
+            iter(j, R0, R1, R3, T{});
+            iter(j + 1, R1, R2, R0, T{});
+            iter(j + 2, R2, R3, R1, F{});
+        } else if (rem == 4) {
+            iter(j, R0, R1, R3, T{});
+            iter(j + 1, R1, R2, R0, T{});
+            iter(j + 2, R2, R3, R1, T{});
+            iter(j + 3, R3, R0, R2, F{});
+        }
+    } else if constexpr (NSET == 3) {
+        for (; j + 4 <= nst; j += 3) {
+            iter(j, R0, R1, R2, T{});
+            iter(j + 1, R1, R2, R0, T{});
+            iter(j + 2, R2, R0, R1, T{});
+        }
+        const int rem = nst - j;  // the last 1 to 3 stages, straight-line
+        if (rem == 1) {
+            iter(j, R0, R1, R2, F{});
+        } else if (rem == 2) {
+            iter(j, R0, R1, R2, T{});
+            iter(j + 1, R1, R2, R0, F{});
+        } else if (rem == 3) {
+            iter(j, R0, R1, R2, T{});
+            iter(j + 1, R1, R2, R0, T{});
+            iter(j + 2, R2, R0, R1, F{});
+        }
+    } else {
+        for (; j + 3 <= nst; j += 2) {
+            iter(j, R0, R1, R1, T{});
+            iter(j + 1, R1, R0, R0, T{});
+        }
+        const int rem = nst - j;  // the last 1 or 2 stages, straight-line
+        if (rem == 1) {
+            iter(j, R0, R1, R1, F{});
+        } else if (rem == 2) {
+            iter(j, R0, R1, R1, T{});
+            iter(j + 1, R1, R0, R0, F{});
+        }
+    }
+
+    // the appended rows into the planes, for the launches that follow (stores issued here, behind no loads)
+    if (nr > 0) {
+        unsigned short* Ku = (unsigned short*)K;
+        unsigned short* Vu = (unsigned short*)V;
+        for (int it = tid; it < nr * 32; it += 512) {
+            const int i = it >> 5, d0 = (it & 31) * 8;
+            *(u16x8*)(Ku + k_off(apf + i, d0)) = *(const u16x8*)&newk[i][d0];
+        }
+        for (int it = tid; it < nr * HD; it += 512) {
+            const int i = it / HD, d = it % HD;
+            Vu[v_off(apf + i, d)] = __builtin_bit_cast(unsigned short, newv[i][d]);
+        }
+    }
 
     // partials: this wave's 32 dims of every row of a present token; m and l from the rows' softmax threads
     const int nrows = 8 * ntok;
@@ -431,8 +603,18 @@ __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part,
 
 }  // namespace
 
-DecodePlan decode_plan(int n, int ntok, int start) {
+DecodePlan decode_plan(int fmt, int n, int ntok, int start) {
     const int kend = n + ntok - 1;
+    if (fmt == 0) {
+        // 64-position stages dealt round robin (neighbouring stages stream from different CUs at once, which keeps
+        // HBM busier than one contiguous range per work-group), at least 2 stages and at most DEC_WG work-groups
+        // per kv head
+        const int s0 = start / KPS_F16 * KPS_F16;
+        const int nu = (kend - s0 + KPS_F16 - 1) / KPS_F16;
+        int g = nu / 2;
+        g = g < 1 ? 1 : g > DEC_WG ? DEC_WG : g;
+        return DecodePlan{0, g, 0, s0, nu};
+    }
     // chunks of at least 128 positions, at most 124 per kv head: 248 work-groups on the 256 CUs, one each. (Measured
     // at 64K positions: 124 chunks of 512 or 544 positions beat 128, 120 and 112 -- the work-group with the most
     // 64-position stages sets the time.)
@@ -456,8 +638,8 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
     const float scale2 = scale * LOG2E;
     dim3 grid(p.nch - p.c0, KVH);
     if (g.fmt == 0)
-        return launch(decode_f16, grid, dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.span, p.nch,
-                      p.c0, ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
+        return launch(decode_f16<DEC_NSET>, grid, dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.s0, p.nu,
+                      ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
     if (fa.ntok) return hipErrorNotSupported;
     return launch(decode_f32, grid, dim3(256), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.span, p.nch, p.c0,
                   ws.part);

@@ -90,7 +90,7 @@ hipError_t traced(mkv_store* h, int kind, F&& fn) {
 
 hipError_t decode_all(mkv_store* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
                       const float* gate, const FusedAppend& fa = FusedAppend{}) {
-    DecodePlan p = decode_plan(n, ntok, start);
+    DecodePlan p = decode_plan(h->g.fmt, n, ntok, start);
     hipError_t e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
         return launch_decode_core(h->g, h->base, layer, q, ntok, n, start, scale, p, h->dws, fa, L);
     });

@@ -46,6 +46,23 @@ __device__ inline float reduce16(float x, Op op) {
     return x;
 }
 
+// Raw buffer access: a 16-byte load whose offset lies past the resource's `bytes` returns zeros without a memory
+// access, which masks lanes or whole loads without a branch (and so without the waits a branch around a load makes
+// the compiler insert).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr unsigned OOB = 0xFFFFFF00u;  // an offset past every plane
+// base and bytes must be wave-uniform; they are read from the first lane so that the resource lives in scalar
+// registers (a resource in vector registers makes the compiler loop over lanes around every load)
+__device__ inline rsrc_t plane_rsrc(const void* base, unsigned bytes) {
+    const unsigned long long a = (unsigned long long)base;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a), hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+    void* b = (void*)(((unsigned long long)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(b, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+__device__ inline half8 bload16(rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 // Work-group barrier for LDS traffic only: waits for this wave's LDS operations, not for its global loads (a
 // __syncthreads() would also wait for every pending global load and drain the loads already in flight).
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

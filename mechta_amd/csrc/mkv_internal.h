@@ -59,8 +59,14 @@ __device__ inline float rope_dim(const float* __restrict__ a, const float* __res
 __host__ __device__ inline int chunk_lo(int c, int span, int nch) {
     return (int)((long long)c * span / nch / KBLK * KBLK);
 }
-// Chunks [c0, c1) are the ones holding a position of [lo, hi) (lo < hi <= the keys' end).
+// Chunks [c0, c1) are the ones holding a position of [lo, hi) (lo < hi <= the keys' end). span == 0 marks an
+// interleaved split (each split holds positions spread over the whole range): every split is a candidate.
 __host__ __device__ inline void chunk_range(int lo, int hi, int span, int nch, int& c0, int& c1) {
+    if (span == 0) {
+        c0 = 0;
+        c1 = nch;
+        return;
+    }
     c0 = (int)((long long)lo * nch / span);  // estimates, then exact by the boundaries
     while (c0 > 0 && chunk_lo(c0, span, nch) > lo) c0--;
     while (c0 + 1 < nch && chunk_lo(c0 + 1, span, nch) <= lo) c0++;
@@ -120,10 +126,14 @@ hipError_t launch_read_rows(const Geom& g, const void* base, int layer, int whic
 hipError_t launch_write_rows(const Geom& g, void* base, int layer, int which, int p0, int p1, const void* src,
                              const Launch& L);
 // Split-K pass and merge of the decode (two kernels).
+// f32 store: contiguous chunks of [0, span) (chunk_lo), chunks below c0 end before `start`.
+// f16 store: span = 0, c0 = 0 and the keys [s0, kend) are nu stages of KPS_F16 positions (s0 = start rounded down to
+// a stage), dealt round robin to nch work-groups, the partial round first.
+constexpr int KPS_F16 = 64;
 struct DecodePlan {
-    int span, nch, c0;  // chunks of [0, span); chunks below c0 end before `start`
+    int span, nch, c0, s0, nu;
 };
-DecodePlan decode_plan(int n, int ntok, int start);
+DecodePlan decode_plan(int fmt, int n, int ntok, int start);
 hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float* q, int ntok, int n, int start,
                               float scale, const DecodePlan& p, const DecodeWs& ws, const FusedAppend& fa,
                               const Launch& L);
