@@ -4,9 +4,11 @@
 Headline workload ("cfg2"): one full-attention layer, f16 KV cache holding 65,536 positions,
 a 4-token MTP verify step = append of the 4 tokens' K/V rows (RoPE + f32->f16) followed by the 4-token GQA split-K
 decode (16 query / 2 KV heads, head_dim 256, causal among the drafts), then 2 drafts rejected: the length is rolled
-back by 2 before the next step's append. One step = one append + one decode + the rollback; the next step starts 2
-positions further (K steps grow the context from 65,536 by 2K positions). Inputs (K/V rows, Q, RoPE tables) are
-seeded N(0,1) values already resident in HBM when the timed region starts.
+back by 2 before the next position's appends. The steps go round the model's 10 full-attention layers, each with
+its own cache (1.35 GB in all, so the K/V bytes come from HBM, not from the 256 MB last-level cache): step i is the
+verify on layer i % 10, and after layer 9 the length is rolled back and the next position starts 2 further. One step
+= one layer's append + decode (+ the rollback every 10 steps). Inputs (K/V rows, Q, RoPE tables) are seeded N(0,1)
+values already resident in HBM when the timed region starts.
 
 Second figure (configs[2], "cfg3"): causal prefill attention of 512 tokens appended to a cache at 28,000 positions
 (28,512 keys), reported as tokens/s.
@@ -43,9 +45,12 @@ def seeded_normal(torch, gen, shape):
     return torch.randn(shape, generator=gen, device="cuda", dtype=torch.float32)
 
 
-def fill_store(torch, mk, st, layer, n_pos, gen, chunk=512):
-    """Appends n_pos seeded tokens through the library's own append path."""
-    tabs = torch.tensor([mk.rope_table(p) for p in range(n_pos)], dtype=torch.float32, device="cuda")
+def rope_tabs(torch, mk, p0, p1):
+    return torch.tensor([mk.rope_table(p) for p in range(p0, p1)], dtype=torch.float32, device="cuda")
+
+
+def fill_store(torch, mk, st, layer, n_pos, gen, tabs, chunk=512):
+    """Appends n_pos seeded tokens through the library's own append path (tabs: RoPE rows of positions 0..n_pos)."""
     for p0 in range(0, n_pos, chunk):
         m = min(chunk, n_pos - p0)
         st.append(layer, p0, seeded_normal(torch, gen, (m, 2, 256)), seeded_normal(torch, gen, (m, 512)),
@@ -53,31 +58,40 @@ def fill_store(torch, mk, st, layer, n_pos, gen, chunk=512):
     st.sync()
 
 
+DEC_LAYERS = 10  # full-attention layers of the model
+
+
 def bench_decode(torch, mk, steps, warmup):
-    N0, NT = 65536, 4
+    """cfg2 steps over DEC_LAYERS layers, each with its own f16 cache at 65,536 positions (1.35 GB in all, far more
+    than the 256 MB last-level cache, so every step streams its layer's K/V from HBM). Step i verifies 4 tokens on
+    layer i % DEC_LAYERS; after the last layer of a position the length is rolled back by 2 (2 drafts rejected) and
+    the next position starts 2 further, as the model's decode does."""
+    N0, NT, L = 65536, 4, DEC_LAYERS
     total = warmup + 2 * steps
-    ctx = ((N0 + 2 * total + NT + 1023) // 1024) * 1024
+    ngroups = (total + L - 1) // L
+    ctx = ((N0 + 2 * ngroups + NT + 1023) // 1024) * 1024
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2026)
-    st = mk.KvStore(1, ctx, mk.F16)
-    fill_store(torch, mk, st, 0, N0, gen)
+    st = mk.KvStore(L, ctx, mk.F16)
+    tabs0 = rope_tabs(torch, mk, 0, N0)
+    for layer in range(L):
+        fill_store(torch, mk, st, layer, N0, gen, tabs0)
+    del tabs0
     # per-step inputs, resident before timing
-    nsteps = warmup + steps + steps
-    kn = seeded_normal(torch, gen, (nsteps, NT, 2, 256))
-    v = seeded_normal(torch, gen, (nsteps, NT, 512))
-    q = seeded_normal(torch, gen, (nsteps, NT, 16, 256))
+    kn = seeded_normal(torch, gen, (total, NT, 2, 256))
+    v = seeded_normal(torch, gen, (total, NT, 512))
+    q = seeded_normal(torch, gen, (total, NT, 16, 256))
     out = torch.empty((NT, 16, 256), device="cuda")
-    tabs = torch.tensor([[mk.rope_table(N0 + 2 * i + t) for t in range(NT)] for i in range(nsteps)],
-                        dtype=torch.float32, device="cuda")
-    pos = N0
+    gtabs = rope_tabs(torch, mk, N0, N0 + 2 * ngroups + NT + 1)
     kend_sum = 0
 
     def step(i):
-        nonlocal pos, kend_sum
-        st.append_decode(0, pos + 1, kn[i], v[i], tabs[i], q[i], out=out)
+        nonlocal kend_sum
+        layer, pos = i % L, N0 + 2 * (i // L)
+        st.append_decode(layer, pos + 1, kn[i], v[i], gtabs[pos + 1 - N0:pos + 1 - N0 + NT], q[i], out=out)
         kend_sum += pos + NT
-        st.set_len(pos + 2)  # 2 of the 3 drafts rejected: roll back before the next append
-        pos += 2
+        if layer == L - 1:
+            st.set_len(pos + 2)  # 2 of the 3 drafts rejected: roll back before the next position's appends
 
     for i in range(warmup):
         step(i)
@@ -93,19 +107,20 @@ def bench_decode(torch, mk, steps, warmup):
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1)
     kend_mean = kend_sum / steps
-    # second pass, same K steps, every kernel bracketed by HIP events (library trace spans)
+    # second pass, the next K steps, every kernel timed by its dispatch (library trace spans)
     st.trace(True)
     for i in range(warmup + steps, warmup + 2 * steps):
         step(i)
     spans = st.trace_read()
     st.trace(False)
     kend_mean2 = (kend_sum - kend_mean * steps) / steps
-    cache_rows = (st.read_rows(0, mk.K, 0, pos + 2), st.read_rows(0, mk.V, 0, pos + 2))
-    last = dict(q=q[warmup + 2 * steps - 1].cpu().numpy(), kn=kn[0].cpu().numpy(), v=v[0].cpu().numpy(),
-                tab=tabs[0].cpu().numpy(), n=pos - 2 + 1)
+    # CPU baseline sample: layer 0's first N0 rows plus room for the 4 appended ones
+    cache_rows = (st.read_rows(0, mk.K, 0, N0), st.read_rows(0, mk.V, 0, N0))
+    last = dict(q=q[total - 1].cpu().numpy(), kn=kn[0].cpu().numpy(), v=v[0].cpu().numpy(),
+                tab=gtabs[1:1 + NT].cpu().numpy(), n=N0 - NT + 1)
     st.close()
     return dict(ms=ms, wall=wall, steps=steps, kend=kend_mean, kend2=kend_mean2, spans=spans, ctx=ctx,
-                cache=cache_rows, last=last)
+                cache=cache_rows, last=last, layers=L)
 
 
 def bench_prefill(torch, mk, steps, warmup):
@@ -114,7 +129,7 @@ def bench_prefill(torch, mk, steps, warmup):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2027)
     st = mk.KvStore(1, ctx, mk.F16)
-    fill_store(torch, mk, st, 0, N0, gen)
+    fill_store(torch, mk, st, 0, N0, gen, rope_tabs(torch, mk, 0, N0))
     kn = seeded_normal(torch, gen, (T, 2, 256))
     v = seeded_normal(torch, gen, (T, 512))
     q = seeded_normal(torch, gen, (T, 16, 256)) / 16.0  # pre-scaled by 1/sqrt(256)
@@ -205,7 +220,7 @@ def main():
         "data": "synthetic (seeded N(0,1) K/V/Q, RoPE tables from rope_table)",
         "config": {"workload": "cfg2: 4-token MTP verify step on one attention layer, f16 KV at 65,536 positions: "
                                "append 4 rows + GQA split-K decode, then 2 drafts rolled back",
-                   "q_heads": 16, "kv_heads": 2, "head_dim": 256, "ctx": dec["ctx"],
+                   "q_heads": 16, "kv_heads": 2, "head_dim": 256, "ctx": dec["ctx"], "layers_rotated": dec["layers"],
                    "keys_per_step_mean": round(dec["kend"], 1)},
         "hbm_gbps_step": round(bytes_rw / (ms_step * 1e-3) / 1e9, 1),
         "kernel_ms": {k: round(v[0] / max(v[1], 1), 5) for k, v in dec["spans"].items()},
