@@ -38,7 +38,50 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy kernel (reference for HBM counter scaling)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="no GPU work: summarize two rocprofv3 --pmc output directories (FETCH_SIZE, WRITE_SIZE) of a "
+                         "--calib-copy run into HBM bytes per dispatch")
     return ap.parse_args()
+
+
+# HBM bytes per launch of the two kernels at the bench's workloads, from the FETCH_SIZE and WRITE_SIZE counters
+# (rocprofv3 --pmc of "bench.py --steps 20 --warmup 2 --no-cpu --calib-copy", summarized by --pmc-summary; the
+# counters are scaled by what they read for the 256 MiB copy of --calib-copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).
+TRAFFIC = {"decode_f16": 143.74e6, "prefill_f16": 545.61e6}
+
+
+def pmc_summary(fetch_dir, write_dir):
+    """Mean FETCH_SIZE / WRITE_SIZE (KiB) per dispatch of each kernel, scaled to bytes by the 256 MiB copy kernel."""
+    import csv
+    import glob
+    import collections
+
+    def load(d):
+        f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)[0]
+        per = collections.defaultdict(list)
+        for r in csv.DictReader(open(f)):
+            per[(r["Kernel_Name"], int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
+        return per
+
+    fetch, write = load(fetch_dir), load(write_dir)
+    copy_bytes = 256 << 20  # the --calib-copy kernel reads and writes 256 MiB (64M floats, grid 16,777,216)
+    cf = [v for (k, g), vs in fetch.items() if g == (64 << 20) // 4 and "elementwise" in k for v in vs]
+    cw = [v for (k, g), vs in write.items() if g == (64 << 20) // 4 and "elementwise" in k for v in vs]
+    f_scale = copy_bytes / (max(cf) * 1024)
+    w_scale = copy_bytes / (max(cw) * 1024)
+    print(f"copy kernel (256 MiB read + 256 MiB written): FETCH_SIZE {max(cf):.0f} KiB -> scale {f_scale:.3f}; "
+          f"WRITE_SIZE {max(cw):.0f} KiB -> scale {w_scale:.3f}")
+    print("| kernel | grid | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | read MB | written MB | HBM MB |")
+    print("|---|---|---|---|---|---|---|---|")
+    for key in sorted(fetch, key=lambda k: -sum(fetch[k]) / len(fetch[k])):
+        name, grid = key
+        if "mkv" not in name or key not in write:
+            continue
+        fk, wk = sum(fetch[key]) / len(fetch[key]), sum(write[key]) / len(write[key])
+        rb, wb = fk * 1024 * f_scale / 1e6, wk * 1024 * w_scale / 1e6
+        short = next((x for x in ("decode_f16", "decode_f32", "decode_combine", "merge_few", "append_kernel",
+                                  "rows_kernel", "prefill_f16") if x in name), name[:40])
+        print(f"| {short} | {grid} | {len(fetch[key])} | {fk:.1f} | {wk:.1f} | {rb:.2f} | {wb:.2f} | {rb + wb:.2f} |")
 
 
 def seeded_normal(torch, gen, shape):
@@ -187,6 +230,9 @@ def cpu_baseline(dec, budget_s):
 
 def main():
     args = parse()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the KV-cache path would "
               f"shard over positions with one small all-gather of split-K partials per step (design only).",
@@ -225,7 +271,7 @@ def main():
         "hbm_gbps_step": round(bytes_rw / (ms_step * 1e-3) / 1e9, 1),
         "kernel_ms": {k: round(v[0] / max(v[1], 1), 5) for k, v in dec["spans"].items()},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC["decode_f16"],
                      "kernel": "decode_f16", "bytes_per_launch": int(core_bytes)},
     }
     if not args.no_prefill:
@@ -236,7 +282,7 @@ def main():
             tf = pf["flops"] / (pf["core_ms"] * 1e-3) / 1e12
             res["roofline_prefill"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_MFMA_PEAK_TFLOPS,
                                        "unit": "TFLOP/s", "frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
-                                       "kernel": "prefill_f16"}
+                                       "traffic": TRAFFIC["prefill_f16"], "kernel": "prefill_f16"}
     if args.calib_copy:
         # plain elementwise copy of a known size: its FETCH_SIZE / WRITE_SIZE counters give the scale from counter
         # units to bytes for the KV kernels' counters in the same run

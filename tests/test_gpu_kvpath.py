@@ -150,8 +150,10 @@ def test_errors(torch_gpu, mk):
 DECODE_CASES = [  # (ctx, n0 positions already in the cache, ntok, start)
     (4096, 1, 1, 0), (4096, 31, 4, 0), (4096, 300, 4, 0), (4096, 1000, 1, 0), (4096, 4092, 4, 0),
     (8192, 4096, 1, 0), (8192, 5000, 4, 0), (8192, 2047, 2, 0), (8192, 3000, 3, 1), (8192, 3000, 4, 700),
-    # chunk sizes that are not a multiple of the 64-key stage (the last stage of a chunk reaches into the next one)
     (20480, 20000, 4, 0), (20480, 17000, 1, 0),
+    # 64-key stages dealt to 124 work-groups per kv head: 1092 stages leave a partial round of 100 > 124 / 2 (whole
+    # stages), 1026 a round of 34 (split into half stages)
+    (70656, 69885, 4, 0), (66560, 65660, 4, 0), (66560, 65600, 1, 3000),
 ]
 
 
@@ -169,7 +171,7 @@ def test_decode_f16(torch_gpu, mk, ctx, n0, ntok, start):
     ex = exact_attention(kc, vc, q, n0, start=start)
     assert_attn_close(out, ex, what="vs f64")
     if ntok == 1:
-        assert_attn_close(out, O.attn_fd(F16, kc, vc, q, n0), what="vs attn_fd")
+        assert_attn_close(out, O.attn_fd(F16, kc, vc, q, n0, start=start), what="vs attn_fd")
 
 
 @pytest.mark.parametrize("ctx,n0,ntok,start", [(4096, 300, 4, 0), (4096, 1000, 1, 0), (8192, 5000, 4, 17),
@@ -199,19 +201,27 @@ def test_decode_gate(torch_gpu, mk):
     assert_attn_close(out, ref, what="gated")
 
 
-def test_append_decode_fused_entry(torch_gpu, mk):
+@pytest.mark.parametrize("ctx,n0", [(4096, 1234), (4096, 1279), (4096, 1282), (4096, 66), (20480, 19199),
+                                    (66560, 65536 + 63)])
+def test_append_decode_fused_entry(torch_gpu, mk, ctx, n0):
+    """The fused entry equals append + decode bit for bit, also when the new rows straddle two 64-key stages (held
+    by different work-groups) or sit in a work-group's first stages."""
     torch = torch_gpu
-    n0 = 1234
+    print(f"fused append+decode ctx={ctx} n0={n0}", flush=True)
     kn, v = kv_inputs(31, 4)
     tab = O.rope_tables(n0 - 1, 4)
     q = q_inputs(32, 4)
-    with mk.KvStore(1, 4096, F16) as a, mk.KvStore(1, 4096, F16) as b:
+    with mk.KvStore(1, ctx, F16) as a, mk.KvStore(1, ctx, F16) as b:
         fill(torch, a, 0, F16, n0 - 1, seed=33)
         fill(torch, b, 0, F16, n0 - 1, seed=33)
         oa = a.append_decode(0, n0, dev(torch, kn), dev(torch, v), dev(torch, tab), dev(torch, q)).cpu().numpy()
         b.append(0, n0 - 1, dev(torch, kn), dev(torch, v), dev(torch, tab))
         ob = b.decode(0, dev(torch, q), n0).cpu().numpy()
+        ka, va = caches_np(a, 0, n0 + 3)
+        kb, vb = caches_np(b, 0, n0 + 3)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb), "fused append wrote other rows"
     assert np.array_equal(oa, ob)
+    assert_attn_close(oa, O.attn_dmx(ka, va, q, n0), what="fused vs oracle")
 
 
 # ------------------------------------------------------------------------------------------------ prefill --------
@@ -305,3 +315,96 @@ def test_prefill_cfg3_sampled_tokens(torch_gpu, mk):
     sel = np.array([0, 1, 15, 16, 63, 64, 200, 255, 256, 400, 510, 511], np.int32)
     ref = O.attn_fa_mx(kc, vc, q, n0 + 1, scale=1.0, sel=sel)
     assert_attn_close(out[sel], ref, what="cfg3 prefill")
+
+
+def seeded_fill(torch, mk, store, layer, n_pos, seed, chunk=512):
+    """Large caches: seeded N(0,1) K/V generated on the device, appended through the library in chunks."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    tab = dev(torch, O.rope_tables(0, n_pos))
+    for p0 in range(0, n_pos, chunk):
+        m = min(chunk, n_pos - p0)
+        kn = torch.randn((m, 2, 256), generator=g, device="cuda")
+        v = torch.randn((m, 512), generator=g, device="cuda")
+        store.append(layer, p0, kn, v, tab[p0:p0 + m])
+    store.sync()
+
+
+def test_decode_cfg1_full_size(torch_gpu, mk):
+    """one token on an f16 cache pre-filled to 4096 positions, append of its row, attention,
+    sigmoid output gate; against the oracle's attn_fd (the reference's 1-token kernel) and f64."""
+    torch = torch_gpu
+    print("decode cfg1 full size", flush=True)
+    n0 = 4096
+    with mk.KvStore(1, 8192, F16) as st:
+        fill(torch, st, 0, F16, n0, seed=960)
+        kn, v = kv_inputs(961, 1)
+        q, qf = q_inputs(962, 1), gate_inputs(963, 1)
+        out = st.append_decode(0, n0 + 1, dev(torch, kn), dev(torch, v), dev(torch, O.rope_tables(n0, 1)),
+                               dev(torch, q), gate_src=dev(torch, qf)).cpu().numpy()
+        kc, vc = caches_np(st, 0, n0 + 1)
+    ref = O.gate(O.attn_fd(F16, kc, vc, q, n0 + 1), qf).reshape(out.shape)
+    assert_attn_close(out, ref, what="cfg1 vs attn_fd + gate")
+    ex = O.gate(exact_attention(kc, vc, q, n0 + 1), qf).reshape(out.shape)
+    assert_attn_close(out, ex, what="cfg1 vs f64")
+
+
+def test_decode_cfg4_full_size(torch_gpu, mk):
+    """the 10 full-attention layers at a 262,144-position context (5.37 GB of f16 K/V), a
+    4-token verify at positions 262,140..262,143 on every layer (append through the fused entry); layers 0, 5 and 9
+    against the oracle, every layer finite; then 2 drafts rolled back and layer 0 re-verified over them."""
+    torch = torch_gpu
+    print("decode cfg4 full size", flush=True)
+    L, ctx = 10, 262144
+    pos = ctx - 4
+    with mk.KvStore(L, ctx, F16) as st:
+        for layer in range(L):
+            seeded_fill(torch, mk, st, layer, pos, seed=970 + layer)
+        kn, v = kv_inputs(981, 4)
+        tab = dev(torch, O.rope_tables(pos, 4))
+        q = q_inputs(982, 4)
+        outs = [st.append_decode(layer, pos + 1, dev(torch, kn), dev(torch, v), tab, dev(torch, q)).cpu().numpy()
+                for layer in range(L)]
+        assert all(np.isfinite(o).all() for o in outs)
+        for layer in (0, 5, 9):
+            kc, vc = caches_np(st, layer, pos + 4)
+            assert_attn_close(outs[layer], O.attn_dmx(kc, vc, q, pos + 1), what=f"cfg4 layer {layer}")
+        st.set_len(pos + 2)
+        kn2, v2 = kv_inputs(983, 2)
+        q2 = q_inputs(984, 2)
+        o2 = st.append_decode(0, pos + 3, dev(torch, kn2), dev(torch, v2), dev(torch, O.rope_tables(pos + 2, 2)),
+                              dev(torch, q2)).cpu().numpy()
+        kc, vc = caches_np(st, 0, pos + 4)
+        assert_attn_close(o2, O.attn_dmx(kc, vc, q2, pos + 3), what="cfg4 after rollback")
+
+
+def test_snapshot_cfg5_full_size(torch_gpu, mk):
+    """f32 caches of 10 layers at 16,384 positions gathered to pinned host memory (671 MB),
+    restored into a fresh store, then a 4-token verify on both: restored rows and outputs bit-identical, one layer's
+    output against the oracle's f32 attn_fd."""
+    torch = torch_gpu
+    print("snapshot cfg5 full size", flush=True)
+    L, p = 10, 16384
+    kn, v = kv_inputs(991, 4)
+    tab = dev(torch, O.rope_tables(p, 4))
+    q = q_inputs(992, 4)
+    with mk.KvStore(L, 17408, F32) as a:
+        for layer in range(L):
+            seeded_fill(torch, mk, a, layer, p, seed=993 + layer)
+        img = a.snapshot(p)
+        a.sync()
+        assert img.numel() == a.snapshot_bytes(p) == L * 2 * p * 512 * 4
+        assert img.is_pinned()
+        rows_a = [caches_np(a, layer, p) for layer in range(L)]
+        outs_a = [a.append_decode(layer, p + 1, dev(torch, kn), dev(torch, v), tab, dev(torch, q)).cpu().numpy()
+                  for layer in range(L)]
+        kc0, vc0 = caches_np(a, 0, p + 4)
+    assert_attn_close(outs_a[0], O.attn_fd(F32, kc0, vc0, q, p + 1), atol=1e-5, rtol=1e-5, what="cfg5 f32 vs attn_fd")
+    with mk.KvStore(L, 17408, F32) as b:
+        b.restore(p, img)
+        b.sync()
+        for layer in range(L):
+            kb, vb = caches_np(b, layer, p)
+            assert np.array_equal(kb, rows_a[layer][0]) and np.array_equal(vb, rows_a[layer][1]), f"layer {layer}"
+            ob = b.append_decode(layer, p + 1, dev(torch, kn), dev(torch, v), tab, dev(torch, q)).cpu().numpy()
+            assert np.array_equal(ob, outs_a[layer]), f"layer {layer}: outputs differ after restore"
