@@ -2,21 +2,20 @@
 //
 // Replaces attn_fd (ops.wgsl:310-394), q_dmx + attn_dmx2 (dmx.rs:19-138) and attn_fd_combine (ops.wgsl:523-538).
 //
-// f16 store (decode_f16): a work-group = (chunk of `ch` positions, kv head); its 4 waves take the chunk's 32-key
-// tiles round robin. The 8 query heads of the kv head times the ntok tokens are 32 query rows (row = t*8 + head,
-// rows of absent tokens are zero), so one wave does, per tile:
-//   S^T[32 keys][32 rows] = K_tile . Q^T   16 x v_mfma_f32_32x32x16_f16 (A = K straight from the tiled plane)
+// f16 store (decode_f16): the keys are 64-position stages dealt round robin to the work-groups of a kv head (plan in
+// decode_plan). The 8 query heads of the kv head times the ntok tokens are 32 query rows (row = t*8 + head, rows of
+// absent tokens are zero). Per stage the 8 waves compute
+//   S[64 keys][32 rows], each wave 16 keys x 128 dims   v_mfma_f32_16x16x32_f16, A = K from the blocked K plane
 //   online softmax of the 32 rows, lazy reference max (moves when first or when the tile max exceeds it by > 8,
 //   as attn_dmx, dmx.rs:72-74), P rounded to f16, l += f32(P)
-//   O[32 rows][256] += P . V_tile           16 x v_mfma_f32_32x32x16_f16 (B = V straight from the grouped plane)
-// K and V tiles are read once per work-group with 16-byte loads, each load instruction covering 2 x 512 contiguous
-// bytes, so the kernel is a coalesced HBM stream; the tile's 32 KB are in flight before the first MFMA.
-// The 4 waves' (m, l, O) are merged in LDS and the work-group writes one partial [m, l, acc[256]] per row.
+//   O[32 rows][32 dims per wave] += P . V      v_mfma_f32_32x32x16_f16, B = V straight from the grouped V plane
+// in a software pipeline with one LDS barrier per stage, two stages of K/V in flight in registers. Each work-group
+// writes one partial [m, l, 0, 0, acc[256]] per row.
 //
-// f32 store (decode_f32): same grid and partials, f32 VALU math with K, V and Q staged through LDS.
+// f32 store (decode_f32): contiguous chunks, f32 VALU math with K, V and Q staged through LDS, same partials.
 //
-// decode_combine: one work-group per (token, head), thread = dim: o = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c
-// over the chunks holding a visible key, then the optional sigmoid output gate (attn_gate, ops.wgsl:171-177).
+// decode_combine: one work-group per (token, head, 64 dims): o = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c
+// over the partials holding a visible key, then the optional sigmoid output gate (attn_gate, ops.wgsl:171-177).
 // Partials keep m in log2 units (scores are pre-multiplied by scale * log2 e).
 #include <type_traits>
 
