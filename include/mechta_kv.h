@@ -54,7 +54,8 @@ typedef struct mkv_store mkv_t;
 #define MKV_E_SIZE (-5)  /* byte count of a snapshot buffer does not match mkv_snapshot_bytes */
 #define MKV_E_HIP (-6)   /* HIP runtime failure (message in mkv_last_error) */
 #define MKV_E_NOMEM (-7) /* device allocation failed */
-#define MKV_E_FMT (-8)   /* operation not available for this KV format */
+#define MKV_E_FMT (-8)   /* operation not available for this KV format, or a root file that does not fit the store */
+#define MKV_E_IO (-9)    /* root file missing, unreadable, truncated or not a root file */
 
 #define MKV_CTX_MIN 4096   /* engine.rs:22 */
 #define MKV_CTX_MAX 262144 /* engine.rs:23 */
@@ -148,6 +149,35 @@ int mkv_trace_read(mkv_t* h, double* ms /*[MKV_SPANS]*/, long* count /*[MKV_SPAN
 /* rope_table(pos) on the host (engine.rs:108-114): tab[0..32) = cos, tab[32..64) = sin of th_i, th_0 = pos,
  * th_{i+1} = th_i * 1e7^(-2/64), all in f32. */
 int mkv_rope_table(int pos, float* tab);
+
+/* Root files: the prefix cache across sessions on disk (write_root_file / read_root_file, session.rs:92-129), byte for
+ * byte the reference's container, so the files are interchangeable with its:
+ *   "MECHTA-ROOT-1\n", u64 p, u64 ns, u64 nk, p x u32 tokens, ns SSM vectors, ns conv vectors, nk x (K vector,
+ *   V vector); a vector is a u64 word count followed by that many 32-bit words; every number little-endian.
+ * The KV vectors are the words read_root gathers for the attention layers (engine.rs:784-802): positions [0, p)
+ * position-major ([pos][kvh][256]), f32 values or pairs of f16 bits, p*512 (f32) or p*256 (f16) words; nk is the
+ * store's layer count. The SSM / conv vectors are the caller's model state (the DeltaNet layers of the reference)
+ * and pass through as opaque 32-bit words.
+ *
+ * mkv_root_key: FNV-1a 64 of the tokens' little-endian bytes (root_key, session.rs:62-66), the key in the file name.
+ * mkv_root_save: gathers positions [0, p) of every layer (waits for the copy into host memory), then writes
+ *   path + ".tmp" and renames it to path (as write_root_file). With background != 0 the file write runs on a thread
+ *   of the handle and mkv_root_save returns once the words are in host memory; mkv_root_wait joins it and returns
+ *   its result (a later mkv_root_save or mkv_destroy joins it too). tokens: p entries; ssm[i], conv[i]: host arrays
+ *   of ssm_words[i], conv_words[i] words (i < ns), copied before the call returns.
+ * mkv_root_info: p, ns and nk of a file, the KV vectors' word count, and (arrays of at least max_ns entries, or
+ *   NULL) the SSM / conv vectors' word counts; checks that the file holds every word its header announces.
+ * mkv_root_load: puts a root file into the store: every layer's positions [0, p) (the length becomes p) from the KV
+ *   vectors, and the tokens / state vectors into the caller's arrays (NULL to skip; sizes from mkv_root_info).
+ *   Refused (MKV_E_FMT, store unchanged) unless nk == layers, p <= ctx and the KV word count matches the format.
+ *   Returns when the store holds the data. */
+uint64_t mkv_root_key(const uint32_t* tokens, size_t n);
+int mkv_root_save(mkv_t* h, const char* path, int p, const uint32_t* tokens, int ns, const float* const* ssm,
+                  const uint64_t* ssm_words, const float* const* conv, const uint64_t* conv_words, int background);
+int mkv_root_wait(mkv_t* h);
+int mkv_root_info(const char* path, int* p, int* ns, int* nk, uint64_t* kv_words, uint64_t* ssm_words,
+                  uint64_t* conv_words, int max_ns);
+int mkv_root_load(mkv_t* h, const char* path, uint32_t* tokens, float* const* ssm, float* const* conv);
 
 #ifdef __cplusplus
 }

@@ -17,13 +17,13 @@ KV_HEADS, Q_HEADS, HEAD_DIM = 2, 16, 256
 CTX_MIN, CTX_MAX = 4096, 262144
 PREFILL_MAX = 512
 
-E_ARG, E_CTX, E_POS, E_LAYER, E_SIZE, E_HIP, E_NOMEM, E_FMT = -1, -2, -3, -4, -5, -6, -7, -8
+E_ARG, E_CTX, E_POS, E_LAYER, E_SIZE, E_HIP, E_NOMEM, E_FMT, E_IO = -1, -2, -3, -4, -5, -6, -7, -8, -9
 
 # every symbol include/mechta_kv.h declares
 SYMBOLS = ["mkv_create", "mkv_destroy", "mkv_set_stream", "mkv_sync", "mkv_last_error", "mkv_info", "mkv_len",
            "mkv_append", "mkv_set_len", "mkv_decode", "mkv_append_decode", "mkv_prefill", "mkv_snapshot_bytes",
            "mkv_snapshot", "mkv_restore", "mkv_read_rows", "mkv_write_rows", "mkv_trace", "mkv_trace_read",
-           "mkv_rope_table"]
+           "mkv_rope_table", "mkv_root_key", "mkv_root_save", "mkv_root_wait", "mkv_root_info", "mkv_root_load"]
 SPAN_KV_WRITE, SPAN_CORE, SPAN_MERGE = 0, 1, 2
 
 
@@ -44,7 +44,7 @@ def lib():
             raise RuntimeError(f"{LIB_PATH} is missing: build it with python -c 'import __graft_entry__ as g; "
                                f"g.build()'")
         L = ctypes.CDLL(LIB_PATH)
-        P, I, F, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+        P, I, F, S, U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_uint64
         sig = {
             "mkv_create": ([ctypes.POINTER(P), I, I, I, P], I),
             "mkv_destroy": ([P], I),
@@ -66,6 +66,12 @@ def lib():
             "mkv_trace": ([P, I], I),
             "mkv_trace_read": ([P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_long)], I),
             "mkv_rope_table": ([I, P], I),
+            "mkv_root_key": ([P, S], U64),
+            "mkv_root_save": ([P, ctypes.c_char_p, I, P, I, P, P, P, P, I], I),
+            "mkv_root_wait": ([P], I),
+            "mkv_root_info": ([ctypes.c_char_p, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I),
+                               ctypes.POINTER(U64), P, P, I], I),
+            "mkv_root_load": ([P, ctypes.c_char_p, P, P, P], I),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -103,6 +109,29 @@ def rope_table(pos):
     buf = (ctypes.c_float * 64)()
     _check(lib().mkv_rope_table(int(pos), buf))
     return list(buf)
+
+
+def root_key(tokens):
+    """FNV-1a 64 of the tokens' little-endian bytes (root_key, session.rs:62-66), computed by the library."""
+    import numpy as np
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    return lib().mkv_root_key(t.ctypes.data_as(ctypes.c_void_p), t.size)
+
+
+def root_info(path):
+    """Counts of a root file: dict(p, ns, nk, kv_words, ssm_words, conv_words)."""
+    p, ns, nk, kw = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_uint64()
+    _check(lib().mkv_root_info(os.fsencode(path), ctypes.byref(p), ctypes.byref(ns), ctypes.byref(nk),
+                               ctypes.byref(kw), None, None, 0))
+    sw = (ctypes.c_uint64 * max(ns.value, 1))()
+    cw = (ctypes.c_uint64 * max(ns.value, 1))()
+    _check(lib().mkv_root_info(os.fsencode(path), None, None, None, None, sw, cw, ns.value))
+    return dict(p=p.value, ns=ns.value, nk=nk.value, kv_words=kw.value, ssm_words=list(sw)[:ns.value],
+                conv_words=list(cw)[:ns.value])
+
+
+def _ptr_array(arrays):
+    return (ctypes.c_void_p * max(len(arrays), 1))(*[a.ctypes.data for a in arrays])
 
 
 class KvStore:
@@ -226,3 +255,30 @@ class KvStore:
 
     def write_rows(self, layer, which, p0, p1, rows):
         _check(lib().mkv_write_rows(self._h, layer, which, p0, p1, _ptr(rows)))
+
+    def root_save(self, path, p, tokens, ssm=(), conv=(), background=False):
+        """Writes a root file (the reference's container) of positions [0, p) of every layer, the p tokens and the
+        caller's state vectors (float32 arrays, ssm[i] with conv[i])."""
+        import numpy as np
+        tok = np.ascontiguousarray(tokens, dtype=np.uint32)
+        assert tok.size == p and len(ssm) == len(conv)
+        ssm = [np.ascontiguousarray(a, dtype=np.float32) for a in ssm]
+        conv = [np.ascontiguousarray(a, dtype=np.float32) for a in conv]
+        sw = (ctypes.c_uint64 * max(len(ssm), 1))(*[a.size for a in ssm])
+        cw = (ctypes.c_uint64 * max(len(conv), 1))(*[a.size for a in conv])
+        _check(lib().mkv_root_save(self._h, os.fsencode(path), p, tok.ctypes.data_as(ctypes.c_void_p), len(ssm),
+                                   _ptr_array(ssm), sw, _ptr_array(conv), cw, 1 if background else 0))
+
+    def root_wait(self):
+        _check(lib().mkv_root_wait(self._h))
+
+    def root_load(self, path):
+        """Puts a root file into the store; returns (p, tokens, ssm list, conv list) of the file."""
+        import numpy as np
+        info = root_info(path)
+        tok = np.empty(info["p"], np.uint32)
+        ssm = [np.empty(n, np.float32) for n in info["ssm_words"]]
+        conv = [np.empty(n, np.float32) for n in info["conv_words"]]
+        _check(lib().mkv_root_load(self._h, os.fsencode(path), tok.ctypes.data_as(ctypes.c_void_p),
+                                   _ptr_array(ssm), _ptr_array(conv)))
+        return info["p"], tok, ssm, conv

@@ -14,31 +14,11 @@
 
 #include "../../include/mechta_kv.h"
 #include "mkv_internal.h"
+#include "mkv_store.h"
 
 using namespace mkv;
 
-struct mkv_store {
-    Geom g;
-    void* base = nullptr;           // layers x {K, V} x 2 planes
-    hipStream_t stream = nullptr;
-    std::vector<int> len;           // written positions per layer
-    DecodeWs dws{nullptr, 0};
-    float* pws = nullptr;           // prefill partials
-    size_t pws_floats = 0;
-    // tracing: events bracketing each kernel launch while on
-    bool tracing = false;
-    struct Span {
-        int kind;
-        hipEvent_t a, b;
-    };
-    std::vector<Span> pending;
-    std::vector<hipEvent_t> pool;
-    double ms[MKV_SPANS] = {0, 0, 0};
-    long count[MKV_SPANS] = {0, 0, 0};
-};
-
-namespace {
-
+namespace mkv {
 thread_local char g_err[512] = "";
 
 int fail(int code, const char* fmt, ...) {
@@ -49,9 +29,13 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-int hip_fail(hipError_t e, const char* what) {
-    return fail(MKV_E_HIP, "%s: %s", what, hipGetErrorString(e));
-}
+int hip_fail(hipError_t e, const char* what) { return fail(MKV_E_HIP, "%s: %s", what, hipGetErrorString(e)); }
+}  // namespace mkv
+
+namespace {
+
+using mkv::fail;
+using mkv::hip_fail;
 
 int check_layer(const mkv_store* h, int layer) {
     if (layer < 0 || layer >= h->g.layers) return fail(MKV_E_LAYER, "layer %d outside [0, %d)", layer, h->g.layers);
@@ -167,6 +151,7 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
 
 int mkv_destroy(mkv_t* h) {
     if (!h) return MKV_OK;
+    root_join(h);
     hipError_t e = hipStreamSynchronize(h->stream);
     free_events(h);
     (void)hipFree(h->base);
@@ -390,7 +375,7 @@ int mkv_restore(mkv_t* h, int p, const void* host, size_t bytes) {
 }
 
 int mkv_read_rows(mkv_t* h, int layer, int which, int p0, int p1, void* dst) {
-    if (!h || !dst) return fail(MKV_E_ARG, "mkv_read_rows: NULL argument");
+    if (!h || (!dst && p1 != p0)) return fail(MKV_E_ARG, "mkv_read_rows: NULL argument");
     if (int rc = check_layer(h, layer)) return rc;
     if (which != MKV_K && which != MKV_V) return fail(MKV_E_ARG, "mkv_read_rows: which = %d", which);
     if (p0 < 0 || p1 < p0 || p1 > h->g.ctx) return fail(MKV_E_POS, "mkv_read_rows: [%d, %d)", p0, p1);
@@ -399,7 +384,7 @@ int mkv_read_rows(mkv_t* h, int layer, int which, int p0, int p1, void* dst) {
 }
 
 int mkv_write_rows(mkv_t* h, int layer, int which, int p0, int p1, const void* src) {
-    if (!h || !src) return fail(MKV_E_ARG, "mkv_write_rows: NULL argument");
+    if (!h || (!src && p1 != p0)) return fail(MKV_E_ARG, "mkv_write_rows: NULL argument");
     if (int rc = check_layer(h, layer)) return rc;
     if (which != MKV_K && which != MKV_V) return fail(MKV_E_ARG, "mkv_write_rows: which = %d", which);
     if (p0 < 0 || p1 < p0 || p1 > h->g.ctx) return fail(MKV_E_POS, "mkv_write_rows: [%d, %d)", p0, p1);

@@ -60,3 +60,62 @@ def exact_attention(kc, vc, q, n, start=0, scale=1.0 / 16):
             w = np.exp(s - s.max())
             out[t, h] = (w @ V[start:e, h // 8]) / w.sum()
     return out
+
+
+# ---- root files (session.rs:92-129), written and parsed here independently of the library ----
+
+ROOT_HEADER = b"MECHTA-ROOT-1\n"
+
+
+def fnv1a64(data: bytes) -> int:
+    """FNV-1a 64 (Fowler/Noll/Vo): offset basis 0xcbf29ce484222325, prime 0x100000001b3, per byte xor then multiply."""
+    x = 0xCBF29CE484222325
+    for b in data:
+        x = ((x ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return x
+
+
+def write_root_py(path, p, tokens, ssm, conv, kv):
+    """A root file as write_root_file lays it out: header, u64 p, ns, nk, u32 tokens, ssm vectors, conv vectors,
+    (K, V) vectors; vector = u64 word count + the words (kv: list of (K words, V words), 32-bit arrays)."""
+    import struct
+    with open(path, "wb") as f:
+        f.write(ROOT_HEADER)
+        f.write(struct.pack("<QQQ", p, len(ssm), len(kv)))
+        f.write(np.asarray(tokens, "<u4").tobytes())
+        for vecs in (ssm, conv):
+            for a in vecs:
+                a = np.ascontiguousarray(a).view("<u4")
+                f.write(struct.pack("<Q", a.size))
+                f.write(a.tobytes())
+        for k, v in kv:
+            for a in (k, v):
+                a = np.ascontiguousarray(a).view("<u4")
+                f.write(struct.pack("<Q", a.size))
+                f.write(a.tobytes())
+
+
+def read_root_py(path):
+    """Parses a root file like read_root_file: (p, tokens, ssm, conv, kv) with 32-bit word arrays (uint32)."""
+    import struct
+    b = open(path, "rb").read()
+    assert b.startswith(ROOT_HEADER)
+    o = len(ROOT_HEADER)
+    p, ns, nk = struct.unpack_from("<QQQ", b, o)
+    o += 24
+    tokens = np.frombuffer(b, "<u4", p, o)
+    o += 4 * p
+
+    def vec():
+        nonlocal o
+        (n,) = struct.unpack_from("<Q", b, o)
+        o += 8
+        a = np.frombuffer(b, "<u4", n, o)
+        o += 4 * n
+        return a
+
+    ssm = [vec() for _ in range(ns)]
+    conv = [vec() for _ in range(ns)]
+    kv = [(vec(), vec()) for _ in range(nk)]
+    assert o == len(b), "trailing bytes"
+    return p, tokens, ssm, conv, kv

@@ -10,6 +10,7 @@ import pytest
 
 import mechta_amd as mk
 from oracle import oracle as O
+from tests.helpers import fnv1a64, write_root_py
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "mechta_kv.h")
@@ -54,3 +55,49 @@ def test_errors_without_gpu():
     assert lib.mkv_create(None, 1, 4096, mk.F16, None) == mk.E_ARG
     assert lib.mkv_decode(None, 0, None, 1, 1, 0, 1.0, None, None) == mk.E_ARG
     assert lib.mkv_snapshot_bytes(None, 10) == 0
+
+
+# ---- root files: key and container parsing (host code only) ----
+
+def test_fnv1a64_published_vectors():
+    # FNV-1a 64 test vectors published with the algorithm (Fowler/Noll/Vo test suite)
+    assert fnv1a64(b"") == 0xCBF29CE484222325
+    assert fnv1a64(b"a") == 0xAF63DC4C8601EC8C
+    assert fnv1a64(b"foobar") == 0x85944171F73967E8
+
+
+def test_root_key_is_fnv1a_of_token_bytes():
+    r = np.random.default_rng(5)
+    for n in (0, 1, 7, 2048):
+        tok = r.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+        assert mk.root_key(tok) == fnv1a64(tok.astype("<u4").tobytes())
+    assert mk.root_key(np.frombuffer(b"foob", "<u4")) == fnv1a64(b"foob")
+
+
+def test_root_info_reads_the_reference_layout(tmp_path):
+    r = np.random.default_rng(6)
+    p, nk = 5, 3
+    tok = np.arange(100, 100 + p, dtype=np.uint32)
+    ssm = [r.standard_normal(7).astype(np.float32), r.standard_normal(0).astype(np.float32)]
+    conv = [r.standard_normal(3).astype(np.float32), r.standard_normal(11).astype(np.float32)]
+    kv = [(r.integers(0, 2**32, p * 256, dtype=np.uint64).astype(np.uint32),
+           r.integers(0, 2**32, p * 256, dtype=np.uint64).astype(np.uint32)) for _ in range(nk)]
+    f = tmp_path / "root.bin"
+    write_root_py(f, p, tok, ssm, conv, kv)
+    info = mk.root_info(f)
+    assert info == dict(p=p, ns=2, nk=nk, kv_words=p * 256, ssm_words=[7, 0], conv_words=[3, 11])
+    b = f.read_bytes()
+    for cut in (3, 14, 20, 38, len(b) - 4 * p * 256 - 1, len(b) - 1):  # truncated anywhere: refused
+        g = tmp_path / f"cut{cut}.bin"
+        g.write_bytes(b[:cut])
+        with pytest.raises(mk.MkvError) as e:
+            mk.root_info(g)
+        assert e.value.code == mk.E_IO
+    g = tmp_path / "bad.bin"
+    g.write_bytes(b"MECHTA-ROOT-2\n" + b[14:])
+    with pytest.raises(mk.MkvError) as e:
+        mk.root_info(g)
+    assert e.value.code == mk.E_IO
+    with pytest.raises(mk.MkvError) as e:
+        mk.root_info(tmp_path / "missing.bin")
+    assert e.value.code == mk.E_IO

@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import (assert_attn_close, exact_attention, gate_inputs, kv_inputs, q_inputs)
+from tests.helpers import (assert_attn_close, exact_attention, gate_inputs, kv_inputs, q_inputs, read_root_py,
+                           write_root_py)
 
 pytestmark = pytest.mark.gpu
 
@@ -408,3 +409,90 @@ def test_snapshot_cfg5_full_size(torch_gpu, mk):
             assert np.array_equal(kb, rows_a[layer][0]) and np.array_equal(vb, rows_a[layer][1]), f"layer {layer}"
             ob = b.append_decode(layer, p + 1, dev(torch, kn), dev(torch, v), tab, dev(torch, q)).cpu().numpy()
             assert np.array_equal(ob, outs_a[layer]), f"layer {layer}: outputs differ after restore"
+
+
+# ------------------------------------------------------------------------------------------------ root files -----
+
+@pytest.mark.parametrize("fmt,p,background", [(F16, 1000, False), (F32, 333, True), (F16, 0, False)])
+def test_root_file_roundtrip(torch_gpu, mk, tmp_path, fmt, p, background):
+    """mkv_root_save writes the reference's container (parsed here independently): the tokens, the opaque state
+    vectors and, per layer, K and V words of [0, p) position-major; mkv_root_load puts it into a fresh store of
+    another ctx: bit-identical rows and the next verify's outputs bit-identical."""
+    torch = torch_gpu
+    print(f"root file fmt={fmt} p={p} background={background}", flush=True)
+    layers = 3
+    r = np.random.default_rng(40)
+    tok = r.integers(0, 248320, p).astype(np.uint32)
+    ssm = [r.standard_normal(n).astype(np.float32) for n in (64, 5)]
+    conv = [r.standard_normal(n).astype(np.float32) for n in (9, 0)]
+    path = tmp_path / f"root-{fmt}-{p}.bin"
+    kn, v = kv_inputs(41, 4)
+    tab = dev(torch, O.rope_tables(p, 4))
+    q = dev(torch, q_inputs(42, 4))
+    with mk.KvStore(layers, 4096, fmt) as a:
+        for l in range(layers):
+            fill(torch, a, l, fmt, p + 3, seed=43 + l)
+        a.set_len(p)
+        a.root_save(path, p, tok, ssm, conv, background=background)
+        if background:
+            a.root_wait()
+        rows_a = [caches_np(a, l, p) for l in range(layers)]
+        outs_a = [a.append_decode(l, p + 1, dev(torch, kn), dev(torch, v), tab, q).cpu().numpy()
+                  for l in range(layers)]
+    fp, ftok, fssm, fconv, fkv = read_root_py(path)
+    assert fp == p and np.array_equal(ftok, tok) and len(fkv) == layers
+    assert all(np.array_equal(x, y.view(np.uint32)) for x, y in zip(fssm + fconv, ssm + conv))
+    for l in range(layers):
+        for which in (0, 1):
+            want = rows_a[l][which].reshape(-1)
+            assert np.array_equal(fkv[l][which], want.view(np.uint32)), f"layer {l} which {which}"
+    with mk.KvStore(layers, 8192, fmt) as b:
+        lp, ltok, lssm, lconv = b.root_load(path)
+        assert lp == p and np.array_equal(ltok, tok)
+        assert all(np.array_equal(x, y) for x, y in zip(lssm + lconv, ssm + conv))
+        assert all(b.length(l) == p for l in range(layers))
+        for l in range(layers):
+            kb, vb = caches_np(b, l, p)
+            assert np.array_equal(kb, rows_a[l][0]) and np.array_equal(vb, rows_a[l][1])
+            ob = b.append_decode(l, p + 1, dev(torch, kn), dev(torch, v), tab, q).cpu().numpy()
+            assert np.array_equal(ob, outs_a[l]), f"layer {l}: outputs differ after the root file"
+    with mk.KvStore(layers + 1, 4096, fmt) as c:  # another layer count: refused, store untouched
+        with pytest.raises(mk.MkvError) as e:
+            c.root_load(path)
+        assert e.value.code == mk.E_FMT and c.length(0) == 0
+    if p:
+        with mk.KvStore(layers, 4096, 1 - fmt) as c:  # the other format: the word count does not match
+            with pytest.raises(mk.MkvError) as e:
+                c.root_load(path)
+            assert e.value.code == mk.E_FMT
+
+
+def test_root_file_written_like_the_reference(torch_gpu, mk, tmp_path):
+    """A root file laid out by an independent writer from the oracle's f16 cache words (what read_root gathers):
+    mkv_root_load puts those words into the store, and attention over them matches the oracle."""
+    torch = torch_gpu
+    p, layers = 700, 2
+    kc = np.zeros((p + 4, 2, 256), np.uint16)
+    vc = np.zeros((p + 4, 2, 256), np.uint16)
+    kvw = []
+    for l in range(layers):
+        kcl, vcl = np.zeros_like(kc), np.zeros_like(vc)
+        kn, v = kv_inputs(60 + l, p)
+        O.append(F16, kcl, vcl, 0, kn, v, O.rope_tables(0, p))
+        kvw.append((kcl[:p].view(np.uint32).reshape(-1), vcl[:p].view(np.uint32).reshape(-1)))
+        if l == 1:
+            kc, vc = kcl, vcl
+    path = tmp_path / "ref.bin"
+    write_root_py(path, p, np.arange(p, dtype=np.uint32), [], [], kvw)
+    kn, v = kv_inputs(70, 4)
+    q = q_inputs(71, 4)
+    with mk.KvStore(layers, 4096, F16) as st:
+        st.root_load(path)
+        for l in range(layers):
+            k_, v_ = caches_np(st, l, p)
+            assert np.array_equal(k_.reshape(-1).view(np.uint32), kvw[l][0])
+            assert np.array_equal(v_.reshape(-1).view(np.uint32), kvw[l][1])
+        out = st.append_decode(1, p + 1, dev(torch, kn), dev(torch, v), dev(torch, O.rope_tables(p, 4)),
+                               dev(torch, q)).cpu().numpy()
+    O.append(F16, kc, vc, p, kn, v, O.rope_tables(p, 4))
+    assert_attn_close(out, O.attn_dmx(kc, vc, q, p + 1), what="decode over a reference-layout root")
