@@ -19,24 +19,59 @@
 namespace mkv {
 namespace {
 
-constexpr int RB = 1;                         // 32-row blocks (4 tokens x 8 heads) per wave
-constexpr int NW = 8;                          // waves per work-group (2 per SIMD)
+#ifndef MKV_PF_RB
+#define MKV_PF_RB 1
+#endif
+#ifndef MKV_PF_NW
+#define MKV_PF_NW 8
+#endif
+constexpr int RB = MKV_PF_RB;                 // 32-row blocks (4 tokens x 8 heads) per wave
+constexpr int NW = MKV_PF_NW;                 // waves per work-group
 constexpr int PT = NW * 4 * RB;               // tokens per work-group
+#ifndef MKV_PF_SUB
+#define MKV_PF_SUB 1
+#endif
+constexpr int SUB = MKV_PF_SUB;               // 32-key subtiles per ring slot (per barrier)
 constexpr int TILE_BYTES = 32 * HD * 2;       // one 32-key K block (or its 4 V groups), f16
-constexpr int SLOT_BYTES = 2 * TILE_BYTES;    // K + V of a tile
-constexpr int NSLOT = 4;                      // LDS ring: 3 tiles in flight while one is computed
+constexpr int SLOT_BYTES = 2 * SUB * TILE_BYTES;  // K blocks, then V groups of a slot
+#ifndef MKV_PF_NSLOT
+#define MKV_PF_NSLOT 4
+#endif
+#ifndef MKV_PF_WGS_PER_CU
+#define MKV_PF_WGS_PER_CU 1
+#endif
+constexpr int NSLOT = MKV_PF_NSLOT;           // LDS ring slots: NSLOT - 1 tiles in flight while one is computed
+constexpr int WGS_PER_CU = MKV_PF_WGS_PER_CU;  // work-groups the plan places per CU
+constexpr int NXCD = 8;                        // accelerator dies (XCDs) of the MI355X, each with its own L2
 
-__device__ inline void wait_tiles(int later) {  // at most `later` tiles (4 direct loads each per wave) pending
-    if (later >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else if (later == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+constexpr int LPT = 2 * SUB * TILE_BYTES / NW / 1024;  // direct loads per slot and wave
+static_assert(NSLOT == 2 || LPT == 4 || LPT == 8, "wait counts below");
+
+__device__ inline void wait_tiles(int later) {  // at most `later` tiles (LPT direct loads each per wave) pending
+    if constexpr (NSLOT == 2) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if constexpr (LPT == 4) {
+        if (later >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else if (later == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+        if (later >= 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (later == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
 }
 
 __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restrict__ kplane,
                                                    const _Float16* __restrict__ vplane, size_t plane_elems,
                                                    const float* __restrict__ q, int T, int n, int start, float scale2,
                                                    int span, int nch, float* __restrict__ part) {
-    const int rb = blockIdx.x, sp = blockIdx.y, kvh = blockIdx.z, tid = threadIdx.x;
+    // XCD-aware order: the dispatcher deals consecutive work-groups round robin to the 8 XCDs (each with its own
+    // L2), so work item W = xcd * (grid / 8) + slot keeps the token blocks of one (split, kv head) -- the
+    // work-groups that stream the same keys -- on one XCD, and each key is fetched into one L2 instead of eight.
+    const int G = gridDim.x, L = blockIdx.x;
+    const int W = G % NXCD == 0 ? (L % NXCD) * (G / NXCD) + L / NXCD : L;
+    const int nblk = (T + PT - 1) / PT;
+    const int rb = W % nblk, sp = (W / nblk) % nch, kvh = W / nblk / nch, tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int h = lane >> 5, r = lane & 31;
     const int t0 = rb * PT + 4 * RB * w;     // this wave's first token; row block b holds tokens t0 + 4b .. +3
@@ -48,10 +83,10 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
     const _Float16* V = vplane + (size_t)kvh * plane_elems;
 
     __shared__ __attribute__((aligned(16))) unsigned char ring[NSLOT * SLOT_BYTES];
-    const int ntiles = (ce - cs + 31) / 32;
-    auto issue = [&](int j) {  // each wave copies 1/NW of tile j's K block and V groups into slot j % NSLOT
-        constexpr int PART_BYTES = TILE_BYTES / NW;
-        const int k0 = cs + 32 * j;
+    const int ntiles = (ce - cs + 32 * SUB - 1) / (32 * SUB);
+    auto issue = [&](int j) {  // each wave copies 1/NW of tile j's K blocks and V groups into slot j % NSLOT
+        constexpr int PART_BYTES = SUB * TILE_BYTES / NW;
+        const int k0 = cs + 32 * SUB * j;
         const unsigned char* ks =
             (const unsigned char*)(K + (size_t)(k0 / KBLK) * (KBLK * HD)) + w * PART_BYTES + lane * 16;
         const unsigned char* vs =
@@ -60,7 +95,7 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
 #pragma unroll
         for (int i = 0; i < PART_BYTES / 1024; i++) dma16(ks + i * 1024, dst + i * 1024);
 #pragma unroll
-        for (int i = 0; i < PART_BYTES / 1024; i++) dma16(vs + i * 1024, dst + TILE_BYTES + i * 1024);
+        for (int i = 0; i < PART_BYTES / 1024; i++) dma16(vs + i * 1024, dst + SUB * TILE_BYTES + i * 1024);
     };
     for (int j = 0; j < NSLOT - 1 && j < ntiles; j++) issue(j);
 
@@ -94,22 +129,25 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
 
     // V rows of the tile past the written length may hold anything: zero them in LDS so that 0 * V stays finite
     auto zero_tail = [&](int j) {
-        unsigned short* Vz = (unsigned short*)(ring + (j % NSLOT) * SLOT_BYTES + TILE_BYTES);
-        const int k0 = cs + 32 * j;
-        for (int i = tid; i < 32 * HD; i += NW * 64)
+        unsigned short* Vz = (unsigned short*)(ring + (j % NSLOT) * SLOT_BYTES + SUB * TILE_BYTES);
+        const int k0 = cs + 32 * SUB * j;
+        for (int i = tid; i < 32 * SUB * HD; i += NW * 64)
             if (k0 + (i >> 11) * 8 + (i & 7) >= kend) Vz[i] = 0;  // group i / 2048, position i % 8 in the group
     };
     for (int j = 0; j < ntiles; j++) {
         wait_tiles(min(ntiles - 1 - j, NSLOT - 2));
         lds_barrier();  // tile j is in LDS for every wave; every wave is done with tile j - 1
         if (j + NSLOT - 1 < ntiles) issue(j + NSLOT - 1);  // into the slot of tile j - 1
-        const int k0 = cs + 32 * j;
-        if (k0 + 32 > kend) {
+        if (cs + 32 * SUB * (j + 1) > kend) {
             zero_tail(j);
             lds_barrier();
         }
-        const unsigned char* Ks = ring + (j % NSLOT) * SLOT_BYTES;
-        const unsigned char* Vs = Ks + TILE_BYTES;
+#pragma unroll
+      for (int u = 0; u < SUB; u++) {
+        const int k0 = cs + 32 * (SUB * j + u);
+        if (k0 >= ce) break;
+        const unsigned char* Ks = ring + (j % NSLOT) * SLOT_BYTES + u * TILE_BYTES;
+        const unsigned char* Vs = ring + (j % NSLOT) * SLOT_BYTES + (SUB + u) * TILE_BYTES;
         f32x16 Scur[RB];
 #pragma unroll
         for (int b = 0; b < RB; b++) Scur[b] = f32x16{};
@@ -169,6 +207,7 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
 #pragma unroll
                 for (int b = 0; b < RB; b++) O[b][nb] = mfma32(pa[b][s2], vb, O[b][nb]);
             }
+      }
     }
 
     // partials of this wave's rows of present tokens: row index t*8 + head of the kv head, rows per kv head = 8T
@@ -199,7 +238,7 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
 PrefillPlan prefill_plan(int T, int n) {
     const int kend = n + T - 1;
     const int blocks = 2 * ((T + PT - 1) / PT);  // work-groups per split
-    int nch = 256 / blocks;                      // about one work-group per CU
+    int nch = 256 * WGS_PER_CU / blocks;         // about WGS_PER_CU work-groups per CU
     const int most = kend / 64;                  // splits of at least 64 positions
     nch = nch > most ? most : nch;
     nch = nch < 1 ? 1 : nch > 16 ? 16 : nch;
@@ -214,7 +253,7 @@ hipError_t launch_prefill(const Geom& g, const void* base, int layer, const floa
     const char* b = (const char*)base;
     const void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
     const void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
-    dim3 grid((T + PT - 1) / PT, p.nch, KVH);
+    dim3 grid((T + PT - 1) / PT * p.nch * KVH);
     return launch(prefill_f16, grid, dim3(NW * 64), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
                   p.nch, ws);
 }
