@@ -150,6 +150,26 @@ int mkv_trace_read(mkv_t* h, double* ms /*[MKV_SPANS]*/, long* count /*[MKV_SPAN
  * th_{i+1} = th_i * 1e7^(-2/64), all in f32. */
 int mkv_rope_table(int pos, float* tab);
 
+/* RoPE table on the device: rows [pos][64] of rope_table (the f32 values mkv_rope_table computes on the host, so
+ * the bits are the same) for every position [0, ctx) of the store, built on the first call (a synchronous upload:
+ * call it once before any graph capture) and kept until mkv_destroy. *tab points at row pos; rows pos + 1 .. follow
+ * it. Use it as the rope_tab of mkv_append / mkv_append_decode instead of uploading tables per step (the reference
+ * writes a table per step, engine.rs:626-630). */
+int mkv_rope_table_dev(mkv_t* h, int pos, const float** tab);
+
+/* The q/k producer in front of the append, one launch for the reference's rmsnorm of q, rmsnorm of k and rope2 of
+ * q (quad.rs:113-115, engine.rs:1210-1212; ops.wgsl:27-57 with the qn / kn uniforms of quad.rs:50, ops.wgsl:275-286)
+ * for ntok tokens at positions pos .. pos + ntok - 1:
+ *   qf: [ntok][16][512] f32 (each head's 256 q values, then its 256 gate values: the attn_q matvec output);
+ *   kb: [ntok][2][256] f32 (the attn_k matvec output); q_norm_w, k_norm_w: [256] (attn_q_norm / attn_k_norm);
+ *   eps: the RMSNorm epsilon (1e-6, engine.rs:12);
+ *   q_out: [ntok][16][256] = rope2(rmsnorm(q)), the q of mkv_decode / mkv_append_decode / mkv_prefill;
+ *   kn_out: [ntok][2][256] = rmsnorm(k), the k_normed of mkv_append / mkv_append_decode.
+ * The sum of squares follows the reference's 256-thread tree reduction; square root and division are correctly
+ * rounded; no product is contracted into an FMA. The RoPE rows come from mkv_rope_table_dev. */
+int mkv_qk_norm_rope(mkv_t* h, int pos, int ntok, const float* qf, const float* kb, const float* q_norm_w,
+                     const float* k_norm_w, float eps, float* q_out, float* kn_out);
+
 /* Root files: the prefix cache across sessions on disk (write_root_file / read_root_file, session.rs:92-129), byte for
  * byte the reference's container, so the files are interchangeable with its:
  *   "MECHTA-ROOT-1\n", u64 p, u64 ns, u64 nk, p x u32 tokens, ns SSM vectors, ns conv vectors, nk x (K vector,

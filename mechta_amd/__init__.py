@@ -23,7 +23,8 @@ E_ARG, E_CTX, E_POS, E_LAYER, E_SIZE, E_HIP, E_NOMEM, E_FMT, E_IO = -1, -2, -3, 
 SYMBOLS = ["mkv_create", "mkv_destroy", "mkv_set_stream", "mkv_sync", "mkv_last_error", "mkv_info", "mkv_len",
            "mkv_append", "mkv_set_len", "mkv_decode", "mkv_append_decode", "mkv_prefill", "mkv_snapshot_bytes",
            "mkv_snapshot", "mkv_restore", "mkv_read_rows", "mkv_write_rows", "mkv_trace", "mkv_trace_read",
-           "mkv_rope_table", "mkv_root_key", "mkv_root_save", "mkv_root_wait", "mkv_root_info", "mkv_root_load"]
+           "mkv_rope_table", "mkv_root_key", "mkv_root_save", "mkv_root_wait", "mkv_root_info", "mkv_root_load",
+           "mkv_rope_table_dev", "mkv_qk_norm_rope"]
 SPAN_KV_WRITE, SPAN_CORE, SPAN_MERGE = 0, 1, 2
 
 
@@ -72,6 +73,8 @@ def lib():
             "mkv_root_info": ([ctypes.c_char_p, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I),
                                ctypes.POINTER(U64), P, P, I], I),
             "mkv_root_load": ([P, ctypes.c_char_p, P, P, P], I),
+            "mkv_rope_table_dev": ([P, I, ctypes.POINTER(P)], I),
+            "mkv_qk_norm_rope": ([P, I, I, P, P, P, P, F, P, P], I),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -128,6 +131,16 @@ def root_info(path):
     _check(lib().mkv_root_info(os.fsencode(path), None, None, None, None, sw, cw, ns.value))
     return dict(p=p.value, ns=ns.value, nk=nk.value, kv_words=kw.value, ssm_words=list(sw)[:ns.value],
                 conv_words=list(cw)[:ns.value])
+
+
+def _device_view(addr, n):
+    """A float32 torch tensor over n floats of device memory the library owns (no copy, no ownership)."""
+    import torch
+
+    class _Mem:  # __cuda_array_interface__ provider
+        __cuda_array_interface__ = {"shape": (n,), "typestr": "<f4", "data": (addr, False), "version": 2}
+
+    return torch.as_tensor(_Mem(), device="cuda")
 
 
 def _ptr_array(arrays):
@@ -255,6 +268,34 @@ class KvStore:
 
     def write_rows(self, layer, which, p0, p1, rows):
         _check(lib().mkv_write_rows(self._h, layer, which, p0, p1, _ptr(rows)))
+
+    def rope_table_dev(self, pos, ntok):
+        """Rows pos .. pos + ntok - 1 of the store's device RoPE table, as a float32 device tensor view [ntok][64]."""
+        import torch
+        ptr = ctypes.c_void_p()
+        _check(lib().mkv_rope_table_dev(self._h, pos, ctypes.byref(ptr)))
+        if not hasattr(self, "_rope_view"):
+            # a tensor over the whole table (its allocation belongs to the store): rows are slices of it
+            base = ctypes.c_void_p()
+            _check(lib().mkv_rope_table_dev(self._h, 0, ctypes.byref(base)))
+            self._rope_base = base.value
+            self._rope_view = _device_view(base.value, self.ctx * 64)
+        off = (ptr.value - self._rope_base) // 4
+        return self._rope_view[off:off + ntok * 64].view(ntok, 64)
+
+    def qk_norm_rope(self, pos, qf, kb, q_norm_w, k_norm_w, eps=1e-6, q_out=None, kn_out=None):
+        """q/k producer: (rope2(rmsnorm(q)) [ntok][16][256], rmsnorm(k) [ntok][2][256]) from qf [ntok][16][512]
+        and kb [ntok][2][256] (device tensors)."""
+        import torch
+        ntok = qf.numel() // (Q_HEADS * 512)
+        if q_out is None:
+            q_out = torch.empty((ntok, Q_HEADS, HEAD_DIM), dtype=torch.float32, device=qf.device)
+        if kn_out is None:
+            kn_out = torch.empty((ntok, KV_HEADS, HEAD_DIM), dtype=torch.float32, device=qf.device)
+        _check(lib().mkv_qk_norm_rope(self._h, pos, ntok, _dev(qf, ntok * 8192, "qf"), _dev(kb, ntok * 512, "kb"),
+                                      _dev(q_norm_w, 256, "q_norm_w"), _dev(k_norm_w, 256, "k_norm_w"), eps,
+                                      _dev(q_out, ntok * 4096, "q_out"), _dev(kn_out, ntok * 512, "kn_out")))
+        return q_out, kn_out
 
     def root_save(self, path, p, tokens, ssm=(), conv=(), background=False):
         """Writes a root file (the reference's container) of positions [0, p) of every layer, the p tokens and the

@@ -157,6 +157,7 @@ int mkv_destroy(mkv_t* h) {
     (void)hipFree(h->base);
     (void)hipFree(h->dws.part);
     if (h->pws) (void)hipFree(h->pws);
+    if (h->rope_dev) (void)hipFree(h->rope_dev);
     delete h;
     return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_destroy");
 }
@@ -448,6 +449,42 @@ int mkv_rope_table(int pos, float* tab) {
         th = th * scale;
     }
     return MKV_OK;
+}
+
+int mkv_rope_table_dev(mkv_t* h, int pos, const float** tab) {
+    if (!h || !tab) return fail(MKV_E_ARG, "mkv_rope_table_dev: NULL argument");
+    if (pos < 0 || pos >= h->g.ctx) return fail(MKV_E_POS, "mkv_rope_table_dev: position %d outside [0, %d)", pos,
+                                              h->g.ctx);
+    if (!h->rope_dev) {
+        std::vector<float> t((size_t)h->g.ctx * 64);
+        for (int p = 0; p < h->g.ctx; p++) mkv_rope_table(p, t.data() + (size_t)p * 64);
+        float* d = nullptr;
+        if (hipMalloc(&d, t.size() * sizeof(float)) != hipSuccess)
+            return fail(MKV_E_NOMEM, "mkv_rope_table_dev: %zu bytes", t.size() * sizeof(float));
+        hipError_t e = hipMemcpy(d, t.data(), t.size() * sizeof(float), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return hip_fail(e, "mkv_rope_table_dev");
+        }
+        h->rope_dev = d;
+    }
+    *tab = h->rope_dev + (size_t)pos * 64;
+    return MKV_OK;
+}
+
+int mkv_qk_norm_rope(mkv_t* h, int pos, int ntok, const float* qf, const float* kb, const float* q_norm_w,
+                     const float* k_norm_w, float eps, float* q_out, float* kn_out) {
+    if (!h || !qf || !kb || !q_norm_w || !k_norm_w || !q_out || !kn_out)
+        return fail(MKV_E_ARG, "mkv_qk_norm_rope: NULL argument");
+    if (ntok < 1 || ntok > MKV_PREFILL_MAX) return fail(MKV_E_ARG, "mkv_qk_norm_rope: ntok %d outside [1, %d]", ntok,
+                                                       MKV_PREFILL_MAX);
+    if (pos < 0 || pos + ntok > h->g.ctx)
+        return fail(MKV_E_POS, "mkv_qk_norm_rope: positions [%d, %d) outside the context %d", pos, pos + ntok,
+                    h->g.ctx);
+    const float* tab = nullptr;
+    if (int rc = mkv_rope_table_dev(h, pos, &tab)) return rc;
+    hipError_t e = launch_qk_produce(ntok, qf, kb, q_norm_w, k_norm_w, eps, tab, q_out, kn_out, Launch{h->stream});
+    return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_qk_norm_rope");
 }
 
 }  // extern "C"

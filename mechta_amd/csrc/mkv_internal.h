@@ -143,6 +143,9 @@ hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, 
 // out[t][head] for t < ntok over the chunks (chunk_lo of span, nch) holding a key of [start, n + t), optional gate.
 hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,
                         float* out, const Launch& L);
+// q/k producer (rmsnorm of the q and k heads, rope2 of q) of ntok tokens; tab: [ntok][64] device RoPE rows.
+hipError_t launch_qk_produce(int ntok, const float* qf, const float* kb, const float* q_w, const float* k_w,
+                             float eps, const float* tab, float* q_out, float* kn_out, const Launch& L);
 // Prefill (f16 store): split-K pass into the partials ws, then launch_merge with the returned plan.
 struct PrefillPlan {
     int span, nch;  // splits of [0, span) as chunk_lo

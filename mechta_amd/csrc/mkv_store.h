@@ -28,6 +28,8 @@ struct mkv_store {
     std::vector<hipEvent_t> pool;
     double ms[MKV_SPANS] = {0, 0, 0};
     long count[MKV_SPANS] = {0, 0, 0};
+    // RoPE table rows of every position [0, ctx) on the device (built on first use from mkv_rope_table)
+    float* rope_dev = nullptr;
     // root file written in the background (mkv_root_save with background != 0) from pinned host memory
     std::thread root_thread;
     int root_rc = 0;

@@ -454,3 +454,44 @@ void orc_gate(const float* att, const float* qf, int ntok, float* out) {
             out[(size_t)t * ORC_H * ORC_D + i] = att[(size_t)t * ORC_H * ORC_D + i] * s;
         }
 }
+
+/* rmsnorm (ops.wgsl:27-57) for rows of 256 values, as the q/k norms call it (uniforms qn / kn, quad.rs:50;
+ * engine.rs:965, :1182; f1 = 1, flag = 1: weight, no gate): one work-group of 256 threads per row, thread t holds
+ * x[t]^2, then the shared-memory tree partial[t] += partial[t + m] for m = 128, 64, .., 1; scale = 1 / sqrt(sum / n +
+ * eps) with a correctly rounded square root and division; y = ((x * scale) * 1) * w, no contraction. */
+static void rmsnorm_row(const float* x, const float* w, float eps, float* y) {
+    float part[256];
+    for (int t = 0; t < 256; t++) part[t] = x[t] * x[t];
+    for (int m = 128; m > 0; m >>= 1)
+        for (int t = 0; t < m; t++) part[t] = part[t] + part[t + m];
+    const float scale = 1.0f / sqrtf(part[0] / 256.0f + eps);
+    for (int t = 0; t < 256; t++) y[t] = (x[t] * scale) * 1.0f * w[t];
+}
+
+void orc_rmsnorm_rows(const float* x, int rows, int step, const float* w, float eps, float* y) {
+    for (int r = 0; r < rows; r++) rmsnorm_row(x + (size_t)r * step, w, eps, y + (size_t)r * 256);
+}
+
+/* The q/k producer of one block of ntok tokens (quad.rs:113-115, engine.rs:1210-1212): q rows qf[t][h][0..256)
+ * (qf = [ntok][16][512], q then gate per head) RMS-normed with q_w and rotated by rope2 (ops.wgsl:275-286: dims
+ * t < 32: x1*c - x2*s and x1*s + x2*c at t + 32, dims >= 64 copied) with token t's table row; k rows kb[t][kvh]
+ * RMS-normed with k_w (their rotation is the append's). */
+void orc_qk_norm_rope(const float* qf, const float* kb, int ntok, const float* q_w, const float* k_w, float eps,
+                      const float* tab /*[ntok][64]*/, float* q_out /*[ntok][16][256]*/, float* kn_out /*[ntok][2][256]*/) {
+    float y[256];
+    for (int t = 0; t < ntok; t++) {
+        const float* tb = tab + (size_t)t * 64;
+        for (int h = 0; h < 16; h++) {
+            rmsnorm_row(qf + ((size_t)t * 16 + h) * 512, q_w, eps, y);
+            float* o = q_out + ((size_t)t * 16 + h) * 256;
+            for (int i = 0; i < 32; i++) {
+                const float x1 = y[i], x2 = y[i + 32], c = tb[i], sn = tb[32 + i];
+                o[i] = x1 * c - x2 * sn;
+                o[i + 32] = x1 * sn + x2 * c;
+            }
+            for (int d = 64; d < 256; d++) o[d] = y[d];
+        }
+        orc_rmsnorm_rows(kb + (size_t)t * 512, 2, 256, k_w, eps, kn_out + (size_t)t * 512);
+    }
+}
+

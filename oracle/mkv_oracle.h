@@ -74,6 +74,14 @@ void orc_gate(const float* att, const float* qf, int ntok, float* out);
 /* Threads used by the OpenMP loops (for the CPU-baseline report). */
 int orc_threads(void);
 
+/* rmsnorm of `rows` rows of 256 values (row r at x + r*step) with weight w (ops.wgsl:27-57, the q/k norm uniforms
+ * of quad.rs:50): the reference's 256-thread tree reduction, correctly rounded sqrt and division. y: [rows][256]. */
+void orc_rmsnorm_rows(const float* x, int rows, int step, const float* w, float eps, float* y);
+/* q/k producer of ntok tokens (quad.rs:113-115): q norm + rope2 (ops.wgsl:275-286) into q_out [ntok][16][256],
+ * k norm into kn_out [ntok][2][256]; qf: [ntok][16][512] (q | gate), kb: [ntok][2][256], tab: [ntok][64]. */
+void orc_qk_norm_rope(const float* qf, const float* kb, int ntok, const float* q_w, const float* k_w, float eps,
+                      const float* tab, float* q_out, float* kn_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,8 @@ def lib():
         _lib.orc_attn_fa_mx.argtypes = [P, P, P, I, I, I, F, I, P, I, P]
         _lib.orc_attn_fa_f32.argtypes = [P, P, P, I, I, I, F, P, I, P]
         _lib.orc_gate.argtypes = [P, P, I, P]
+        _lib.orc_rmsnorm_rows.argtypes = [P, I, I, P, F, P]
+        _lib.orc_qk_norm_rope.argtypes = [P, P, I, P, P, F, P, P, P]
         _lib.orc_threads.restype = I
     return _lib
 
@@ -138,6 +140,27 @@ def gate(att, qf):
     out = np.empty_like(att)
     lib().orc_gate(_p(att), _p(qf), ntok, _p(out))
     return out
+
+
+def rmsnorm_rows(x, w, eps=1e-6, step=256):
+    """rmsnorm (ops.wgsl:27-57) of the 256-value rows of x (row r at flat offset r*step) with weight w."""
+    x = _c(x, np.float32).reshape(-1)
+    rows = (x.size - 256) // step + 1
+    out = np.empty((rows, 256), np.float32)
+    lib().orc_rmsnorm_rows(_p(x), rows, int(step), _p(_c(w, np.float32)), float(eps), _p(out))
+    return out
+
+
+def qk_norm_rope(qf, kb, q_w, k_w, tab, eps=1e-6):
+    """q/k producer (quad.rs:113-115): (q normed + rotated [ntok][16][256], k normed [ntok][2][256])."""
+    qf = _c(qf, np.float32).reshape(-1, 16, 512)
+    ntok = qf.shape[0]
+    kb = _c(kb, np.float32).reshape(ntok, 2, 256)
+    q_out = np.empty((ntok, 16, 256), np.float32)
+    kn_out = np.empty((ntok, 2, 256), np.float32)
+    lib().orc_qk_norm_rope(_p(qf), _p(kb), ntok, _p(_c(q_w, np.float32)), _p(_c(k_w, np.float32)), float(eps),
+                           _p(_c(tab, np.float32).reshape(ntok, 64)), _p(q_out), _p(kn_out))
+    return q_out, kn_out
 
 
 def threads():

@@ -496,3 +496,47 @@ def test_root_file_written_like_the_reference(torch_gpu, mk, tmp_path):
                                dev(torch, q)).cpu().numpy()
     O.append(F16, kc, vc, p, kn, v, O.rope_tables(p, 4))
     assert_attn_close(out, O.attn_dmx(kc, vc, q, p + 1), what="decode over a reference-layout root")
+
+
+# ------------------------------------------------------------------------------------------------ q/k producer ---
+
+def producer_inputs(seed, ntok):
+    r = np.random.default_rng(seed)
+    return (r.standard_normal((ntok, 16, 512)).astype(np.float32), r.standard_normal((ntok, 2, 256)).astype(np.float32),
+            r.uniform(0.5, 1.5, 256).astype(np.float32), r.uniform(0.5, 1.5, 256).astype(np.float32))
+
+
+@pytest.mark.parametrize("pos,ntok", [(0, 1), (4096, 1), (65532, 4), (1000, 512), (66000, 37)])
+def test_qk_norm_rope_bit_exact(torch_gpu, mk, pos, ntok):
+    """The producer (rmsnorm of q and k, rope2 of q) bit-identical to the oracle's restatement, with the device
+    RoPE rows bit-identical to rope_table."""
+    torch = torch_gpu
+    print(f"qk producer pos={pos} ntok={ntok}", flush=True)
+    qf, kb, qw, kw = producer_inputs(1000 + ntok, ntok)
+    with mk.KvStore(1, 66560, F16) as st:
+        tab = st.rope_table_dev(pos, ntok)
+        assert np.array_equal(tab.cpu().numpy(), O.rope_tables(pos, ntok))
+        q, kn = st.qk_norm_rope(pos, dev(torch, qf), dev(torch, kb), dev(torch, qw), dev(torch, kw))
+        q, kn = q.cpu().numpy(), kn.cpu().numpy()
+    oq, okn = O.qk_norm_rope(qf, kb, qw, kw, O.rope_tables(pos, ntok))
+    assert np.array_equal(kn, okn), "k norm"
+    assert np.array_equal(q, oq), "q norm + rope"
+
+
+def test_producer_feeds_the_verify(torch_gpu, mk):
+    """producer -> fused append + decode with the device RoPE rows: the appended rows are the oracle's append of the
+    oracle's normed k, the output the oracle's attn_dmx over the oracle's q."""
+    torch = torch_gpu
+    n0, ntok = 3000, 4
+    qf, kb, qw, kw = producer_inputs(1100, ntok)
+    v = np.random.default_rng(1101).standard_normal((ntok, 512)).astype(np.float32)
+    with mk.KvStore(1, 4096, F16) as st:
+        fill(torch, st, 0, F16, n0, seed=1102)
+        q, kn = st.qk_norm_rope(n0, dev(torch, qf), dev(torch, kb), dev(torch, qw), dev(torch, kw))
+        out = st.append_decode(0, n0 + 1, kn, dev(torch, v), st.rope_table_dev(n0, ntok), q).cpu().numpy()
+        kc, vc = caches_np(st, 0, n0 + ntok)
+    oq, okn = O.qk_norm_rope(qf, kb, qw, kw, O.rope_tables(n0, ntok))
+    kc2, vc2 = kc.copy(), vc.copy()
+    O.append(F16, kc2, vc2, n0, okn, v, O.rope_tables(n0, ntok))
+    assert np.array_equal(kc, kc2) and np.array_equal(vc, vc2)
+    assert_attn_close(out, O.attn_dmx(kc, vc, oq, n0 + 1), what="producer + verify")

@@ -262,3 +262,64 @@ def test_gate_closed_form():
     assert np.allclose(O.gate(att, qf), 0.0, atol=1e-30)
     qf[:, :, :256] = 1e9  # the q half of qf is not read
     assert np.allclose(O.gate(att, qf), 0.0, atol=1e-30)
+
+
+# ---- q/k producer: rmsnorm (ops.wgsl:27-57) and rope2 (ops.wgsl:275-286) ----
+
+def test_rmsnorm_closed_forms():
+    w = np.ones(256, np.float32)
+    for c in (1.0, 2.0, 0.5, -4.0):  # constant rows, eps 0: sum = 256 c^2, scale = 1/|c| exactly
+        y = O.rmsnorm_rows(np.full(256, c, np.float32), w, eps=0.0)
+        assert np.array_equal(y[0], np.full(256, math.copysign(1.0, c), np.float32))
+    x = np.random.default_rng(90).standard_normal(256).astype(np.float32)
+    assert np.array_equal(O.rmsnorm_rows(x, 2 * w)[0], 2 * O.rmsnorm_rows(x, w)[0])  # the weight is a last product
+
+
+def test_rmsnorm_is_the_256_thread_tree():
+    # x[1]^2 + x[129]^2 meet first in the reference's tree (m = 128), then join 2^24: the sum is 2^24 + 2 exactly,
+    # where a running sum would round 2^24 + 1 back to 2^24 twice
+    x = np.zeros(256, np.float32)
+    x[0], x[1], x[129] = 4096.0, 1.0, 1.0
+    w = np.random.default_rng(91).uniform(0.5, 1.5, 256).astype(np.float32)
+    s = np.float32(2**24 + 2)
+    scale = np.float32(1.0) / np.sqrt(s / np.float32(256.0) + np.float32(1e-6))  # IEEE f32 ops
+    assert np.array_equal(O.rmsnorm_rows(x, w, eps=1e-6)[0], (x * scale) * w)
+    run = np.float32(0)
+    for v in x:
+        run = np.float32(run + v * v)
+    assert run == np.float32(2**24)  # the sequential order would differ
+
+
+def test_rmsnorm_vs_float64():
+    r = np.random.default_rng(92)
+    x = (r.standard_normal((64, 256)) * r.uniform(1e-3, 1e3, (64, 1))).astype(np.float32)
+    w = r.uniform(0.5, 1.5, 256).astype(np.float32)
+    y = O.rmsnorm_rows(x, w, eps=1e-6)
+    x64 = x.astype(np.float64)
+    ex = x64 / np.sqrt((x64 * x64).mean(1, keepdims=True) + 1e-6) * w
+    assert np.abs(y - ex).max() <= 3e-7 * np.abs(ex).max()
+    # rows at a stride (q rows of qf: 256 q values then 256 gate values)
+    qf = r.standard_normal((3, 512)).astype(np.float32)
+    assert np.array_equal(O.rmsnorm_rows(qf, w, step=512), O.rmsnorm_rows(qf[:, :256], w))
+
+
+def test_qk_norm_rope_position_zero_and_rotation():
+    r = np.random.default_rng(93)
+    ntok = 3
+    qf = r.standard_normal((ntok, 16, 512)).astype(np.float32)
+    kb = r.standard_normal((ntok, 2, 256)).astype(np.float32)
+    qw = r.uniform(0.5, 1.5, 256).astype(np.float32)
+    kw = r.uniform(0.5, 1.5, 256).astype(np.float32)
+    qn = O.rmsnorm_rows(qf.reshape(-1), qw, step=512).reshape(ntok, 16, 256)
+    q0, k0 = O.qk_norm_rope(qf, kb, qw, kw, np.tile(O.rope_table(0), (ntok, 1)))
+    assert np.array_equal(q0, qn)  # cos 0 = 1, sin 0 = 0: no rotation (x*1 - y*0 is exact)
+    assert np.array_equal(k0, O.rmsnorm_rows(kb.reshape(-1), kw).reshape(ntok, 2, 256))
+    pos = 5000
+    tab = O.rope_tables(pos, ntok)
+    q1, k1 = O.qk_norm_rope(qf, kb, qw, kw, tab)
+    assert np.array_equal(k1, k0)  # k is not rotated here (the append rotates it)
+    assert np.array_equal(q1[:, :, 64:], qn[:, :, 64:])
+    a, b = qn[:, :, :32].astype(np.float64), qn[:, :, 32:64].astype(np.float64)
+    c, s = tab[:, None, :32].astype(np.float64), tab[:, None, 32:].astype(np.float64)
+    assert np.allclose(q1[:, :, :32], a * c - b * s, atol=1e-6)  # rotation of each pair (i, i + 32) by th_i
+    assert np.allclose(q1[:, :, 32:64], a * s + b * c, atol=1e-6)
