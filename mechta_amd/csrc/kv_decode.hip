@@ -9,8 +9,9 @@
 //   online softmax of the 32 rows, lazy reference max (moves when first or when the tile max exceeds it by > 8,
 //   as attn_dmx, dmx.rs:72-74), P rounded to f16, l += f32(P)
 //   O[32 rows][32 dims per wave] += P . V      v_mfma_f32_32x32x16_f16, B = V straight from the grouped V plane
-// in a software pipeline with one LDS barrier per stage, two stages of K/V in flight in registers. Each work-group
-// writes one partial [m, l, 0, 0, acc[256]] per row.
+// in a software pipeline with one LDS barrier per stage: K is loaded two stages ahead (for the S MFMAs, which run
+// one stage ahead of the softmax) and V one stage ahead, about one stage of bytes in flight (from HBM that streams
+// faster than two or three). Each work-group writes one partial [m, l, 0, 0, acc[256]] per row.
 //
 // f32 store (decode_f32): contiguous chunks, f32 VALU math with K, V and Q staged through LDS, same partials.
 //
@@ -30,9 +31,9 @@ constexpr int KPS = KPS_F16;                   // keys per stage of the decode r
 #endif
 constexpr int DEC_WG = MKV_DEC_WG;             // most work-groups per kv head (2 x 124 on the 256 CUs)
 #ifndef MKV_DEC_NSET
-#define MKV_DEC_NSET 3
+#define MKV_DEC_NSET 0
 #endif
-constexpr int DEC_NSET = MKV_DEC_NSET;         // register sets of the decode pipeline
+constexpr int DEC_NSET = MKV_DEC_NSET;         // register sets of the decode pipeline; 0 = staggered K / V streams
 constexpr int PS_STRIDE = KPS + 8;             // halves per P row in LDS (conflict-free 16-byte reads)
 constexpr int QS_STRIDE = HD + 8;              // halves per Q row in LDS
 constexpr int NEWMAX = 4;                      // appended rows per call
@@ -45,7 +46,8 @@ struct StageRegs {
     half8 v[4];
 };
 
-// NSET register sets of stage operands (2 to 4): NSET - 1 stages in flight ahead of the one computed.
+// NSET register sets of stage operands (2 to 4): NSET - 1 stages in flight ahead of the one computed; NSET = 0:
+// K two stages ahead and V one stage ahead in two sets each.
 template <int NSET>
 __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane, _Float16* __restrict__ vplane,
                                                   size_t plane_elems, const float* __restrict__ q, int ntok, int n,
@@ -98,15 +100,21 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     const int ceK = (kend + KBLK - 1) / KBLK * KBLK, ceV = (kend + VGRP - 1) / VGRP * VGRP;
     const unsigned kofs = (unsigned)(((kkey / KBLK) * (KBLK * HD) + (kkey % KBLK) * 8 + (16 * dh + g4) * (KBLK * 8)) * 2);
     const unsigned vofs = (unsigned)((h * (VGRP * HD) + (32 * w + r) * VGRP) * 2);
-    auto load = [&](int j, StageRegs& R) {
+    auto load_k = [&](int j, StageRegs& R) {
         const int k0 = kbase(j);  // a multiple of 64: the stage starts a K block and a V group
-        const int len = klen(j);
-        const rsrc_t kr = plane_rsrc(K + (size_t)k0 * HD, (unsigned)(max(min(ceK - k0, len), 0) * (HD * 2)));
-        const rsrc_t vr = plane_rsrc(V + (size_t)k0 * HD, (unsigned)(max(min(ceV - k0, len), 0) * (HD * 2)));
+        const rsrc_t kr = plane_rsrc(K + (size_t)k0 * HD, (unsigned)(max(min(ceK - k0, klen(j)), 0) * (HD * 2)));
 #pragma unroll
         for (int s = 0; s < 4; s++) R.k[s] = bload16(kr, kofs + s * (4 * KBLK * 8 * 2));
+    };
+    auto load_v = [&](int j, StageRegs& R) {
+        const int k0 = kbase(j);
+        const rsrc_t vr = plane_rsrc(V + (size_t)k0 * HD, (unsigned)(max(min(ceV - k0, klen(j)), 0) * (HD * 2)));
 #pragma unroll
         for (int s2 = 0; s2 < 4; s2++) R.v[s2] = bload16(vr, vofs + s2 * (2 * VGRP * HD * 2));
+    };
+    auto load = [&](int j, StageRegs& R) {
+        load_k(j, R);
+        load_v(j, R);
     };
     // Fused append (mkv_append_decode). The new rows [apf, apl) of the stages this work-group owns (at most two
     // stages hold new rows) are computed into LDS (the same arithmetic as append_kernel) and patched into the K and V
@@ -147,12 +155,19 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     // three stages in flight from the start; loads of stages past this work-group's last are out of range and move
     // no bytes, so no load is behind a branch (a branch around loads makes the compiler's wait counts pessimistic)
     StageRegs R0, R1, R2, R3;
-    load(0, R0);
-    if constexpr (NSET > 2) load(1, R1);
-    if constexpr (NSET > 3) load(2, R2);
+    if constexpr (NSET == 0) {  // staggered streams: K two stages ahead, V one (R0/R1 hold K, R2/R3 hold V)
+        load_k(0, R0);
+        load_k(1, R1);
+        load_v(0, R2);
+    } else {
+        load(0, R0);
+        if constexpr (NSET > 2) load(1, R1);
+        if constexpr (NSET > 3) load(2, R2);
+    }
     if (nr > 0) {
         // the direct loads precede the 4 Q and the stage loads; then every wave's LDS data is in
-        static_assert(NSET >= 2 && NSET <= 4, "wait counts below");
+        static_assert(NSET == 0 || (NSET >= 2 && NSET <= 4), "wait counts below");
+        if constexpr (NSET == 0) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
         if constexpr (NSET == 2) asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
         if constexpr (NSET == 3) asm volatile("s_waitcnt vmcnt(20)\n\ts_barrier" ::: "memory");
         if constexpr (NSET == 4) asm volatile("s_waitcnt vmcnt(28)\n\ts_barrier" ::: "memory");
@@ -309,7 +324,34 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     using T = std::true_type;
     using F = std::false_type;
     int j = 0;
-    if constexpr (NSET == 4) {
+    if constexpr (NSET == 0) {
+        // iteration j: K of stage j + 2 and V of stage j + 1 load; S of j + 1 (K loaded one iteration ago); P.V of
+        // j (V loaded one iteration ago): one stage of bytes in flight, each operand a whole iteration ahead
+        auto iter2 = [&](int j, StageRegs& Kn, const StageRegs& K1, StageRegs& Vn, const StageRegs& V0, auto has_next) {
+            const int buf = j & 1;
+            load_k(j + 2, Kn);
+            load_v(j + 1, Vn);
+            if constexpr (decltype(has_next)::value) {
+                auto store_s = s_part(j + 1, K1, buf ^ 1);
+                softmax(j, buf);
+                store_s();
+            } else {
+                softmax(j, buf);
+            }
+            lds_barrier();
+            pv(j, buf, V0);
+        };
+        for (; j + 2 < nst; j += 2) {
+            iter2(j, R0, R1, R3, R2, T{});
+            iter2(j + 1, R1, R0, R2, R3, T{});
+        }
+        if (nst - j == 1) {
+            iter2(j, R0, R1, R3, R2, F{});
+        } else if (nst - j == 2) {
+            iter2(j, R0, R1, R3, R2, T{});
+            iter2(j + 1, R1, R0, R2, R3, F{});
+        }
+    } else if constexpr (NSET == 4) {
         for (; j + 5 <= nst; j += 4) {
             iter(j, R0, R1, R3, T{});
             iter(j + 1, R1, R2, R0, T{});
