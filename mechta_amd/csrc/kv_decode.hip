@@ -603,43 +603,55 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
     }
 }
 
-// Merge for few chunks (prefill splits): work-group = (token, head), thread = dim; all chunks of the row are loaded
-// in one round trip.
-__global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part, int rpk, int n, int start, int span,
-                                                 int nch, const float* __restrict__ gate, float* __restrict__ out) {
-    const int t = blockIdx.x / QH, head = blockIdx.x % QH, d = threadIdx.x;
+// Merge for few chunks (prefill splits): a work-group of 256 threads merges 4 rows (token, head), 64 threads per
+// row, 4 dims per thread (16-byte loads); every chunk of the row is loaded in one round trip.
+__global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part, int rpk, int ntok, int n, int start,
+                                                 int span, int nch, const float* __restrict__ gate,
+                                                 float* __restrict__ out) {
+    const int rowid = blockIdx.x * 4 + (threadIdx.x >> 6);  // t * 16 + head
+    if (rowid >= ntok * QH) return;
+    const int t = rowid / QH, head = rowid % QH, d0 = (threadIdx.x & 63) * 4;
     const int kvh = head / GQA, row = t * GQA + head % GQA;
     const float* p = part + ((size_t)kvh * rpk + row) * nch * PART;
     int c0, c1;  // chunks holding a key of [start, n + t)
     chunk_range(start, n + t, span, nch, c0, c1);
-    float mj[MERGE_FEW], lj[MERGE_FEW], aj[MERGE_FEW];
+    float mj[MERGE_FEW], lj[MERGE_FEW];
+    float4 aj[MERGE_FEW];
     float M = NEG_INF;
 #pragma unroll
     for (int j = 0; j < MERGE_FEW; j++) {
         const int c = c0 + j;
         mj[j] = NEG_INF;
-        lj[j] = aj[j] = 0.f;
+        lj[j] = 0.f;
+        aj[j] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (c < c1) {
             const float* pc = p + (size_t)c * PART;
             mj[j] = pc[0];
             lj[j] = pc[1];
-            aj[j] = pc[PACC + d];
+            aj[j] = *(const float4*)(pc + PACC + d0);
         }
         M = fmaxf(M, mj[j]);
     }
-    float L = 0.f, acc = 0.f;
+    float L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int j = 0; j < MERGE_FEW; j++) {
         const float e = mj[j] == NEG_INF ? 0.f : exp2f(mj[j] - M);
         L += e * lj[j];
-        acc += e * aj[j];
+        acc.x += e * aj[j].x;
+        acc.y += e * aj[j].y;
+        acc.z += e * aj[j].z;
+        acc.w += e * aj[j].w;
     }
-    float o = acc / L;
+    float4 o = make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
     if (gate) {
-        const float g = gate[((size_t)t * QH + head) * 512 + 256 + d];
-        o = o * (1.f / (1.f + expf(-g)));
+        const float4 g = *(const float4*)(gate + ((size_t)t * QH + head) * 512 + 256 + d0);
+        o.x *= 1.f / (1.f + expf(-g.x));
+        o.y *= 1.f / (1.f + expf(-g.y));
+        o.z *= 1.f / (1.f + expf(-g.z));
+        o.w *= 1.f / (1.f + expf(-g.w));
     }
-    out[((size_t)t * QH + head) * HD + d] = o;
+    *(float4*)(out + ((size_t)t * QH + head) * HD + d0) = o;
 }
 
 }  // namespace
@@ -690,7 +702,8 @@ hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, 
                         float* out, const Launch& L) {
     if (nch > 16 * MERGE_J) return hipErrorInvalidValue;
     if (nch <= MERGE_FEW)
-        return launch(merge_few, dim3(ntok * QH), dim3(256), L, part, rpk, n, start, span, nch, gate, out);
+        return launch(merge_few, dim3((ntok * QH + 3) / 4), dim3(256), L, part, rpk, ntok, n, start, span, nch, gate,
+                      out);
     return launch(decode_combine, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, span, nch, gate, out);
 }
 
