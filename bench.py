@@ -11,7 +11,8 @@ verify on layer i % 10, and after layer 9 the length is rolled back and the next
 values already resident in HBM when the timed region starts.
 
 Second figure (configs[2], "cfg3"): causal prefill attention of 512 tokens appended to a cache at 28,000 positions
-(28,512 keys), reported as tokens/s.
+(28,512 keys), reported as tokens/s. Side figures: cfg1 (configs[0], 1 token at 4,096 positions with the output gate,
+µs per step) and cfg4 (configs[3], the 10 layers at 262,144 positions, µs per position and the K+V read rate).
 
 Prints ONE JSON line. value = microseconds per cfg2 step (lower is better). roofline = the decode kernel's achieved
 HBM bandwidth (algorithmic K+V bytes it must read / its mean launch duration, from HIP events bracketing each launch
@@ -36,6 +37,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the cfg1 / cfg4 side measurements")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy kernel (reference for HBM counter scaling)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -206,6 +208,67 @@ def bench_prefill(torch, mk, steps, warmup):
     return dict(ms=ms, tok_s=T / (ms * 1e-3), flops=flops, core_ms=core_ms, core_launches=spans["core"][1] / steps)
 
 
+def bench_cfg1(torch, mk, steps):
+    """1 query token on an f16 cache of 4096 positions, append + decode + gate, µs per step
+    (each step appends at the same position: the same work every step)."""
+    N0 = 4096
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2030)
+    st = mk.KvStore(1, 8192, mk.F16)
+    fill_store(torch, mk, st, 0, N0, gen, rope_tabs(torch, mk, 0, N0))
+    kn, v = seeded_normal(torch, gen, (1, 2, 256)), seeded_normal(torch, gen, (1, 512))
+    q, gate = seeded_normal(torch, gen, (1, 16, 256)), seeded_normal(torch, gen, (1, 16, 512))
+    tab = rope_tabs(torch, mk, N0, N0 + 1)
+    out = torch.empty((1, 16, 256), device="cuda")
+    for _ in range(10):
+        st.append_decode(0, N0 + 1, kn, v, tab, q, out=out, gate_src=gate)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        st.append_decode(0, N0 + 1, kn, v, tab, q, out=out, gate_src=gate)
+    e1.record()
+    torch.cuda.synchronize()
+    st.close()
+    return e0.elapsed_time(e1) / steps * 1000
+
+
+def bench_cfg4(torch, mk, positions):
+    """the 10 attention layers at a 262,144-position context, a 4-token verify per layer (the
+    store of 5.37 GB), `positions` positions of 10 layer steps each with the rollback of 2 drafts; µs per position
+    (all 10 layers) and the K+V read rate."""
+    L, ctx, NT = 10, 262144, 4
+    pos0 = ctx - 4 - 2 * positions
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2031)
+    st = mk.KvStore(L, ctx, mk.F16)
+    tabs = rope_tabs(torch, mk, 0, ctx)
+    for layer in range(L):
+        fill_store(torch, mk, st, layer, pos0, gen, tabs)
+    kn, v = seeded_normal(torch, gen, (NT, 2, 256)), seeded_normal(torch, gen, (NT, 512))
+    q = seeded_normal(torch, gen, (NT, 16, 256))
+    out = torch.empty((NT, 16, 256), device="cuda")
+
+    def position(pos):
+        for layer in range(L):
+            st.append_decode(layer, pos + 1, kn, v, tabs[pos + 1:pos + 1 + NT], q, out=out)
+        st.set_len(pos + 2)
+
+    position(pos0)  # warm-up position
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    keys = 0
+    for i in range(1, positions):
+        position(pos0 + 2 * i)
+        keys += (pos0 + 2 * i + NT) * L
+    e1.record()
+    torch.cuda.synchronize()
+    st.close()
+    us = e0.elapsed_time(e1) / (positions - 1) * 1000
+    return us, keys * 2048 / (positions - 1) / (us * 1e-6) / 1e9
+
+
 def cpu_baseline(dec, budget_s):
     """The oracle's attn_dmx + append on the bench's own cache, on this host's cores."""
     import numpy as np
@@ -283,6 +346,11 @@ def main():
             res["roofline_prefill"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_MFMA_PEAK_TFLOPS,
                                        "unit": "TFLOP/s", "frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
                                        "traffic": TRAFFIC["prefill_f16"], "kernel": "prefill_f16"}
+    if not args.no_extra:
+        res["cfg1_us_per_step"] = round(bench_cfg1(torch, mk, 200), 2)
+        us4, gbs4 = bench_cfg4(torch, mk, 20)
+        res["cfg4_us_per_position_10_layers"] = round(us4, 1)
+        res["cfg4_kv_read_gbps"] = round(gbs4, 1)
     if args.calib_copy:
         # plain elementwise copy of a known size: its FETCH_SIZE / WRITE_SIZE counters give the scale from counter
         # units to bytes for the KV kernels' counters in the same run
