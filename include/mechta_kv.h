@@ -20,10 +20,10 @@
  * is the rollback of rejected MTP drafts (the reference rolls back by starting the next step at pos + na + 1 and
  * overwriting, quad.rs:320, session.rs:396-401: the next append here overwrites the same rows).
  *
- * Layout (f16): per (layer, K|V, kv head) one contiguous plane of ctx*256 halves. K planes are tiled in blocks of 32
- * positions, [pos/32][d/8][pos%32][8]; V planes in groups of 8 positions, [pos/8][d][pos%8]. Both are the operand
- * layouts of the CDNA4 32x32x16 f16 MFMA, so attention streams them with 16-byte loads straight into matrix operands.
- * f32 planes are [pos][256]. mkv_read_rows / mkv_write_rows convert to and from the reference's position-major
+ * Layout: per (layer, K|V, kv head) one contiguous plane of ctx*256 elements. f16: K planes are tiled in blocks of 32
+ * positions, [pos/32][d/8][pos%32][8]; V planes in groups of 8 positions, [pos/8][d][pos%8]. f32: K [pos/32][d/4]
+ * [pos%32][4], V [pos/4][d][pos%4]. These are the operand layouts of the CDNA4 32x32x16 f16 and 32x32x2 f32 MFMAs,
+ * so attention streams them with 16-byte loads straight into matrix operands. mkv_read_rows / mkv_write_rows convert to and from the reference's position-major
  * layout ([pos][kvh][256], kv.wgsl:7-8), e.g. for the reference's root files.
  */
 #ifndef MECHTA_KV_H

@@ -2,7 +2,7 @@
 //
 // Append replaces the reference's writer kernels kv_rope / kv_rope2 / kv_copy (kv.wgsl:19-42) for the f16 cache and
 // rope / rope2 / copy (ops.wgsl:141-162, 275-286) for the f32 cache. One launch writes K and V of all ntok tokens:
-// work items [0, nk) are K items (token, kv head, 8 dims), the rest V items (V group of 8 positions, kv head, dim).
+// work items [0, nk) are K items (token, kv head, 8 dims), the rest V items (V group of positions, kv head, dim).
 #include "mkv_internal.h"
 
 namespace mkv {
@@ -33,22 +33,23 @@ __global__ void __launch_bounds__(256) append_kernel(void* __restrict__ kplane0,
             unsigned short* kp = (unsigned short*)(kh ? kplane1 : kplane0);
             *(u16x8*)(kp + k_off(p, d0)) = w;
         } else {
-            float* kp = (float*)(kh ? kplane1 : kplane0) + (size_t)p * HD + d0;
-            *(float4*)kp = make_float4(r[0], r[1], r[2], r[3]);
-            *(float4*)(kp + 4) = make_float4(r[4], r[5], r[6], r[7]);
+            float* kp = (float*)(kh ? kplane1 : kplane0);
+            *(float4*)(kp + k_off32(p, d0)) = make_float4(r[0], r[1], r[2], r[3]);
+            *(float4*)(kp + k_off32(p, d0 + 4)) = make_float4(r[4], r[5], r[6], r[7]);
         }
         return;
     }
     id -= nk;
+    // V item: group g (relative to the first group touched), kv head kh, dim d; a whole group is one 16-byte store
+    constexpr int VG = FMT == 0 ? VGRP : VGRP32;
+    if (id >= ng * KVH * HD) return;
+    int gi = id / (KVH * HD), kh = (id / HD) % KVH, d = id % HD;
+    int g = pos / VG + gi;
+    int p0 = max(pos, g * VG), p1 = min(pos + ntok, g * VG + VG);
+    const float* src = v + (size_t)kh * HD + d;  // v[t][kh*256 + d], t = p - pos
     if (FMT == 0) {
-        // V item: group g (relative to the first group touched), kv head kh, dim d
-        if (id >= ng * KVH * HD) return;
-        int gi = id / (KVH * HD), kh = (id / HD) % KVH, d = id % HD;
-        int g = pos / VGRP + gi;
-        int p0 = max(pos, g * VGRP), p1 = min(pos + ntok, g * VGRP + VGRP);
         unsigned short* vp = (unsigned short*)(kh ? vplane1 : vplane0);
-        const float* src = v + (size_t)kh * HD + d;  // v[t][kh*256 + d], t = p - pos
-        if (p0 == g * VGRP && p1 == g * VGRP + VGRP) {
+        if (p0 == g * VG && p1 == g * VG + VG) {
             u16x8 w;
 #pragma unroll
             for (int j = 0; j < 8; j++) w[j] = f2h(src[(size_t)(p0 + j - pos) * (KVH * HD)]);
@@ -57,11 +58,14 @@ __global__ void __launch_bounds__(256) append_kernel(void* __restrict__ kplane0,
             for (int p = p0; p < p1; p++) vp[v_off(p, d)] = f2h(src[(size_t)(p - pos) * (KVH * HD)]);
         }
     } else {
-        // V item (f32): token t, kv head kh, 4 dims
-        if (id >= ntok * KVH * (HD / 4)) return;
-        int t = id / (KVH * HD / 4), kh = (id / (HD / 4)) % KVH, d0 = (id % (HD / 4)) * 4;
-        float4 x = *(const float4*)(v + (size_t)t * (KVH * HD) + kh * HD + d0);
-        *(float4*)((float*)(kh ? vplane1 : vplane0) + (size_t)(pos + t) * HD + d0) = x;
+        float* vp = (float*)(kh ? vplane1 : vplane0);
+        if (p0 == g * VG && p1 == g * VG + VG) {
+            const size_t st = KVH * HD;
+            const size_t o = (size_t)(p0 - pos) * st;
+            *(float4*)(vp + v_off32(p0, d)) = make_float4(src[o], src[o + st], src[o + 2 * st], src[o + 3 * st]);
+        } else {
+            for (int p = p0; p < p1; p++) vp[v_off32(p, d)] = src[(size_t)(p - pos) * (KVH * HD)];
+        }
     }
 }
 
@@ -75,7 +79,7 @@ __global__ void __launch_bounds__(256) rows_kernel(T* __restrict__ plane0, T* __
     if (id >= total) return;
     int d = id % HD, kh = (id / HD) % KVH, p = p0 + (int)(id / (KVH * HD));
     T* plane = kh ? plane1 : plane0;
-    size_t o = fmt == 1 ? (size_t)p * HD + d : (which == 0 ? k_off(p, d) : v_off(p, d));
+    size_t o = fmt == 1 ? (which == 0 ? k_off32(p, d) : v_off32(p, d)) : (which == 0 ? k_off(p, d) : v_off(p, d));
     if (DIR == 0) rows[id] = plane[o];
     else plane[o] = rows[id];
 }
@@ -90,8 +94,9 @@ hipError_t launch_append(const Geom& g, void* base, int layer, int pos, int ntok
     void* v0 = b + g.plane(layer, 1, 0) * g.plane_bytes();
     void* v1 = b + g.plane(layer, 1, 1) * g.plane_bytes();
     int nk = ntok * KVH * 32;
-    int ng = (pos + ntok - 1) / VGRP - pos / VGRP + 1;
-    int nv = g.fmt == 0 ? ng * KVH * HD : ntok * KVH * (HD / 4);
+    const int vg = plane_unit(g.fmt, 1);
+    int ng = (pos + ntok - 1) / vg - pos / vg + 1;
+    int nv = ng * KVH * HD;
     int blocks = (nk + nv + 255) / 256;
     return launch(g.fmt == 0 ? append_kernel<0> : append_kernel<1>, dim3(blocks), dim3(256), L, k0, k1, v0, v1, pos,
                   ntok, kn, v, tab, nk, ng);

@@ -1,0 +1,211 @@
+// kv_attn32.hip -- attention over the f32 store on the fp32 matrix cores: the decode of 1-4 tokens (the reference's
+// exact-f32 attn_fd applied per token with the drafts' causal mask, ops.wgsl:310-394, quad.rs:127-131) and the block
+// prefill (attn_fa, ops.wgsl:540-651), one kernel for both.
+//
+// Work-group (block of 4 tokens, key split, kv head): 32 query rows (token * 8 + head) against the split's keys in
+// tiles of 32 keys, 4 waves. Per tile, wave w
+//   S^T[32 keys][32 rows] over dims 64w .. 64w+63    32 x v_mfma_f32_32x32x2_f32, A = K straight from HBM, B = Q (LDS)
+//   the four partial S^T summed through LDS ((w0 + w1) + (w2 + w3), the same order in every wave)
+//   exact-max online softmax of the 32 rows (each wave redundantly: 16 scores per lane)
+//   O[32 rows][dims 64w .. 64w+63] += P . V           32 x v_mfma_f32_32x32x2_f32, A = P (the S^T registers), B = V
+// The 32x32 accumulator layout gives lane l (half s = l / 32) row l % 32 and keys 8a + 4s + b (register 4a + b).
+// Those are the keys the A operand of the P.V MFMAs needs in that lane, so P never leaves the registers, and they are
+// four consecutive keys per register quad: with V stored [pos/4][d][pos%4] each quad's operand is one 16-byte load.
+// K is stored [pos/32][d/4][pos%32][4], so a lane's 16-byte K load is 4 dims of key l % 32 and a wave's load is two
+// 512-byte runs. Tiles are double-buffered in registers: the loads of tile j + 1 fly while tile j computes.
+#include "mkv_device.h"
+
+namespace mkv {
+namespace {
+
+constexpr int TILE = 32;                       // keys per tile: one K block, eight V groups
+constexpr unsigned TILE_BYTES = TILE * HD * 4;  // 32 KB of each plane
+constexpr int QPAD = HD + 4;                   // LDS row of Q (floats): rows 4 banks apart
+
+__device__ inline f32x16 mfma32f(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+__device__ inline f32x4 bload4f(rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+struct Tile {
+    f32x4 k[8];  // K: dims 64w + 8m + 4s .. +3 of key l % 32 (m = 0..7)
+    f32x4 v[8];  // V: keys 8q + 4s .. +3 of dim 64w + 32c + l % 32 (index 4c + q)
+};
+
+__global__ void __launch_bounds__(256) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
+                                                size_t plane_elems, const float* __restrict__ q, int T, int n,
+                                                int start, float scale2, int span, int nch, int c0, int nrb, int rpk,
+                                                float* __restrict__ part) {
+    // XCD-aware order: consecutive work-groups go round robin to the 8 XCDs, so work item W = (L % 8) (G / 8) + L / 8
+    // puts the token blocks that stream the same keys on one XCD's L2
+    const int G = gridDim.x, L = blockIdx.x;
+    const int W = G % NXCD == 0 ? (L % NXCD) * (G / NXCD) + L / NXCD : L;
+    const int ncg = nch - c0;
+    const int rb = W % nrb, c = c0 + (W / nrb) % ncg, kvh = W / nrb / ncg;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, s = lane >> 5, r32 = lane & 31;
+    const int t0 = 4 * rb, nt = min(4, T - t0);
+    const int kend = n + T - 1;  // keys of the whole call
+    const int cs = chunk_lo(c, span, nch), ce = c + 1 < nch ? chunk_lo(c + 1, span, nch) : kend;
+    const int lo = max(cs, start / TILE * TILE), hi = min(ce, n + t0 + nt - 1);  // hi: the block's last key + 1
+    const int ntile = hi > lo ? (hi - lo + TILE - 1) / TILE : 0;
+
+    __shared__ float qs[ROWS][QPAD];
+    __shared__ f32x4 sx[2][4][4][64];  // partial S^T: [tile parity][wave][register quad][lane]
+    for (int i = tid; i < ROWS * HD / 4; i += 256) {
+        const int row = i / (HD / 4), d4 = (i % (HD / 4)) * 4, t = t0 + (row >> 3);
+        f32x4 x = f32x4{};
+        if (t < T) x = *(const f32x4*)(q + ((size_t)t * QH + kvh * GQA + (row & 7)) * HD + d4);
+        *(f32x4*)&qs[row][d4] = x;
+    }
+    __syncthreads();
+
+    // tile j of this split starts at key lo + 32j, at the same byte offset j * 32 KB in both planes; loads of tile
+    // ntile (the prefetch after the last) lie past the resources and return zeros without a memory access
+    const unsigned rbytes = (unsigned)ntile * TILE_BYTES;
+    const rsrc_t kr = plane_rsrc(kplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
+    const rsrc_t vr = plane_rsrc(vplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
+    const unsigned kofs = ((16 * w + s) * (TILE * 4) + r32 * 4) * 4;  // + m * 2 * 512 B
+    const unsigned vofs = (s * (4 * HD) + (64 * w + r32) * 4) * 4;    // + q * 2 * 4 KB + c * 32 dims * 16 B
+    auto load = [&](Tile& X, int j) {
+        const unsigned base = (unsigned)j * TILE_BYTES;
+#pragma unroll
+        for (int m = 0; m < 8; m++) X.k[m] = bload4f(kr, base + kofs + m * (2 * TILE * 4 * 4));
+#pragma unroll
+        for (int cq = 0; cq < 8; cq++)
+            X.v[cq] = bload4f(vr, base + vofs + (cq & 3) * (2 * 4 * HD * 4) + (cq >> 2) * (32 * 4 * 4));
+    };
+
+    const int vis = n + t0 + (r32 >> 3);  // lane's row sees keys < vis
+    float m_run = NEG_INF, l_run = 0.f;
+    f32x16 O[2] = {f32x16{}, f32x16{}};
+    auto step = [&](Tile& X, int j) {
+        const int k0 = lo + j * TILE;
+        f32x16 S = f32x16{};
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const f32x4 qv = *(const f32x4*)&qs[r32][64 * w + 8 * m + 4 * s];
+#pragma unroll
+            for (int b = 0; b < 4; b++) S = mfma32f(X.k[m][b], qv[b], S);
+        }
+        const int pb = j & 1;
+#pragma unroll
+        for (int a = 0; a < 4; a++) sx[pb][w][a][lane] = f32x4{S[4 * a], S[4 * a + 1], S[4 * a + 2], S[4 * a + 3]};
+        lds_barrier();  // parity buffers: tile j + 2 writes pb again only after every wave passed tile j + 1's barrier
+        float sv[16];
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const f32x4 p0 = sx[pb][0][a][lane], p1 = sx[pb][1][a][lane];
+            const f32x4 p2 = sx[pb][2][a][lane], p3 = sx[pb][3][a][lane];
+#pragma unroll
+            for (int b = 0; b < 4; b++) sv[4 * a + b] = (p0[b] + p1[b]) + (p2[b] + p3[b]);
+        }
+        // exact-max online softmax in log2 units; masked scores are -inf (selected, never computed from K)
+        float mt = NEG_INF;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int key = k0 + 8 * (i >> 2) + 4 * s + (i & 3);
+            sv[i] = (key >= start && key < vis) ? sv[i] * scale2 : NEG_INF;
+            mt = fmaxf(mt, sv[i]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m_run, mt);
+        const float base = mn == NEG_INF ? 0.f : mn;
+        const float cf = m_run == NEG_INF ? 0.f : exp2f(m_run - mn);
+        float ls = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            sv[i] = exp2f(sv[i] - base);
+            ls += sv[i];
+        }
+        ls += __shfl_xor(ls, 32);
+        l_run = l_run * cf + ls;
+        m_run = mn;
+        // rescale O: register i of this lane holds row 8(i/4) + 4s + i%4, whose factor lane (that row) holds
+        if (__builtin_amdgcn_ballot_w64(cf != 1.f)) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float f = __shfl(cf, 8 * (i >> 2) + 4 * s + (i & 3));
+                O[0][i] *= f;
+                O[1][i] *= f;
+            }
+        }
+        // keys past the block's last (unwritten or stale rows) have P = 0 and must not bring NaN in through V
+        if (k0 + TILE > hi) {
+#pragma unroll
+            for (int cq = 0; cq < 8; cq++)
+#pragma unroll
+                for (int b = 0; b < 4; b++)
+                    if (k0 + 8 * (cq & 3) + 4 * s + b >= hi) X.v[cq][b] = 0.f;
+        }
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++)
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) O[cc] = mfma32f(sv[4 * qq + b], X.v[4 * cc + qq][b], O[cc]);
+    };
+
+    Tile A, B;
+    load(A, 0);
+    for (int j = 0; j < ntile; j += 2) {
+        load(B, j + 1);
+        step(A, j);
+        if (j + 1 >= ntile) break;
+        load(A, j + 2);
+        step(B, j + 1);
+    }
+
+    // partials of the rows of present tokens: [kvh][row < rpk][chunk < nch][PART], row = token * 8 + head
+    const size_t rbase = (size_t)kvh * rpk + (size_t)t0 * GQA;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int row = 8 * (i >> 2) + 4 * s + (i & 3);
+        if (t0 + (row >> 3) < T) {
+            float* p = part + ((rbase + row) * nch + c) * PART + PACC + 64 * w + r32;
+            p[0] = O[0][i];
+            p[32] = O[1][i];
+        }
+    }
+    if (w == 0 && s == 0 && t0 + (r32 >> 3) < T) {
+        float* p = part + ((rbase + r32) * nch + c) * PART;
+        p[0] = m_run;
+        p[1] = l_run;
+    }
+}
+
+}  // namespace
+
+Attn32Plan attn32_plan(int T, int n, int start) {
+    const int kend = n + T - 1;
+    const int nrb = (T + 3) / 4;
+    int nch;
+    if (T <= 4) {
+        // decode: splits of at least 128 positions, at most 124 per kv head (248 work-groups on the 256 CUs)
+        nch = kend / 128;
+        nch = nch > 124 ? 124 : nch;
+    } else {
+        // prefill: about two work-groups per CU, splits of at least 128 positions, at most 16 (one merge round trip)
+        nch = 512 / (nrb * KVH);
+        const int most = kend / 128;
+        nch = nch > most ? most : nch > 16 ? 16 : nch;
+    }
+    nch = nch < 1 ? 1 : nch;
+    int c0, c1;  // splits wholly below `start` get no work-group
+    chunk_range(start, kend, kend, nch, c0, c1);
+    return Attn32Plan{kend, nch, c0, nrb};
+}
+
+hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
+                           float scale, const Attn32Plan& p, int rpk, float* part, const Launch& L) {
+    if (g.fmt != 1) return hipErrorNotSupported;
+    const char* b = (const char*)base;
+    const float* kp = (const float*)(b + g.plane(layer, 0, 0) * g.plane_bytes());
+    const float* vp = (const float*)(b + g.plane(layer, 1, 0) * g.plane_bytes());
+    dim3 grid(p.nrb * (p.nch - p.c0) * KVH);
+    return launch(attn_f32, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span, p.nch,
+                  p.c0, p.nrb, rpk, part);
+}
+
+}  // namespace mkv

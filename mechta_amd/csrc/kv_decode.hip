@@ -13,7 +13,7 @@
 // one stage ahead of the softmax) and V one stage ahead, about one stage of bytes in flight (from HBM that streams
 // faster than two or three). Each work-group writes one partial [m, l, 0, 0, acc[256]] per row.
 //
-// f32 store (decode_f32): contiguous chunks, f32 VALU math with K, V and Q staged through LDS, same partials.
+// The f32 store has its own kernel (kv_attn32.hip) and shares the merges below.
 //
 // decode_combine: one work-group per (token, head, 64 dims): o = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c
 // over the partials holding a visible key, then the optional sigmoid output gate (attn_gate, ops.wgsl:171-177).
@@ -38,7 +38,7 @@ constexpr int PS_STRIDE = KPS + 8;             // halves per P row in LDS (confl
 constexpr int QS_STRIDE = HD + 8;              // halves per Q row in LDS
 constexpr int NEWMAX = 4;                      // appended rows per call
 constexpr int MERGE_FEW = 16;  // chunks of the one-lane-per-dim merge
-constexpr int MERGE_J = 9;  // chunks per merge lane: 16 lanes x 9 >= the at most 130 chunks of decode_plan
+constexpr int MERGE_J = 9;  // chunks per merge lane: 16 lanes x 9 >= the at most 124 splits of a decode plan
 
 // One stage of this wave's registers: K operands (16 keys x 128 dims) and V operands (64 keys x 32 dims).
 struct StageRegs {
@@ -433,104 +433,6 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     }
 }
 
-// f32 store: VALU flash decode, 32-key tiles staged in LDS; thread (row, 4 keys) for S, thread = dim for P.V.
-__global__ void __launch_bounds__(256) decode_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
-                                                  size_t plane_elems, const float* __restrict__ q, int ntok, int n,
-                                                  int start, float scale2, int span, int nch, int c0,
-                                                  float* __restrict__ part) {
-    const int kvh = blockIdx.y, c = c0 + blockIdx.x, tid = threadIdx.x;
-    const int kend = n + ntok - 1;
-    const int cs = chunk_lo(c, span, nch), ce = c + 1 < nch ? chunk_lo(c + 1, span, nch) : kend;
-    const float* K = kplane + (size_t)kvh * plane_elems;
-    const float* V = vplane + (size_t)kvh * plane_elems;
-    const int nrows = 8 * ntok;
-    __shared__ float qs[ROWS][HD + 1];
-    __shared__ float kv[32][HD + 1];
-    __shared__ float ps[ROWS][33];
-    __shared__ float sm_m[ROWS], sm_l[ROWS], sm_c[ROWS];
-    for (int i = tid; i < ROWS * HD; i += 256) {
-        int row = i / HD, d = i % HD;
-        int t = row >> 3;
-        qs[row][d] = t < ntok ? q[((size_t)t * QH + kvh * GQA + (row & 7)) * HD + d] : 0.f;
-    }
-    if (tid < ROWS) {
-        sm_m[tid] = NEG_INF;
-        sm_l[tid] = 0.f;
-    }
-    float acc[ROWS];
-#pragma unroll
-    for (int i = 0; i < ROWS; i++) acc[i] = 0.f;
-    const int srow = tid >> 3, sq = tid & 7;  // S: row srow, keys 4sq .. 4sq+3
-    for (int k0 = cs; k0 < ce; k0 += 32) {
-        __syncthreads();
-        for (int i = tid; i < 32 * HD / 4; i += 256) {
-            int key = i / (HD / 4), d4 = (i % (HD / 4)) * 4;
-            float4 x = *(const float4*)(K + (size_t)(k0 + key) * HD + d4);
-            kv[key][d4] = x.x; kv[key][d4 + 1] = x.y; kv[key][d4 + 2] = x.z; kv[key][d4 + 3] = x.w;
-        }
-        __syncthreads();
-        float s4[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int d = 0; d < HD; d++) {
-            float qv = qs[srow][d];
-#pragma unroll
-            for (int j = 0; j < 4; j++) s4[j] += qv * kv[4 * sq + j][d];
-        }
-        const int vis = n + (srow >> 3);
-        float mt = NEG_INF;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            int key = k0 + 4 * sq + j;
-            s4[j] = (key < vis && key >= start && key < ce) ? s4[j] * scale2 : NEG_INF;
-            mt = fmaxf(mt, s4[j]);
-        }
-        mt = fmaxf(mt, __shfl_xor(mt, 1));
-        mt = fmaxf(mt, __shfl_xor(mt, 2));
-        mt = fmaxf(mt, __shfl_xor(mt, 4));
-        float mo = sm_m[srow];
-        float mx = fmaxf(mo, mt);
-        float sum = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float p = s4[j] > NEG_INF ? exp2f(s4[j] - mx) : 0.f;
-            ps[srow][4 * sq + j] = p;
-            sum += p;
-        }
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
-        sum += __shfl_xor(sum, 4);
-        __syncthreads();  // everyone has read sm_m[srow] and K
-        if (sq == 0) {
-            float cf = mo == NEG_INF ? 0.f : exp2f(mo - mx);
-            sm_c[srow] = cf;
-            sm_m[srow] = mx;
-            sm_l[srow] = sm_l[srow] * cf + sum;
-        }
-        for (int i = tid; i < 32 * HD / 4; i += 256) {
-            int key = i / (HD / 4), d4 = (i % (HD / 4)) * 4;
-            float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (k0 + key < kend) x = *(const float4*)(V + (size_t)(k0 + key) * HD + d4);
-            kv[key][d4] = x.x; kv[key][d4 + 1] = x.y; kv[key][d4 + 2] = x.z; kv[key][d4 + 3] = x.w;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int row = 0; row < ROWS; row++) acc[row] *= sm_c[row];
-        for (int j = 0; j < 32; j++) {
-            float v = kv[j][tid];
-#pragma unroll
-            for (int row = 0; row < ROWS; row++) acc[row] += ps[row][j] * v;
-        }
-    }
-    __syncthreads();
-    for (int row = 0; row < nrows; row++) {
-        float* p = part + ((size_t)(kvh * ROWS + row) * nch + c) * PART;
-        p[PACC + tid] = acc[row];
-        if (tid == 0) {
-            p[0] = sm_m[row];
-            p[1] = sm_l[row];
-        }
-    }
-}
-
 // Merge of the split-K partials: work-group (token, head, quarter of the dims); its 256 threads are 16 chunk lanes x
 // 16 dim lanes (4 dims each), so every chunk's 64 dims are one coalesced 256-byte read and all chunks are in flight at
 // once; the 16 chunk lanes are then summed in LDS.
@@ -656,29 +558,15 @@ __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part,
 
 }  // namespace
 
-DecodePlan decode_plan(int fmt, int n, int ntok, int start) {
+DecodePlan decode_plan(int n, int ntok, int start) {
+    // 64-position stages dealt round robin (neighbouring stages stream from different CUs at once, which keeps HBM
+    // busier than one contiguous range per work-group), at least 2 stages and at most DEC_WG work-groups per kv head
     const int kend = n + ntok - 1;
-    if (fmt == 0) {
-        // 64-position stages dealt round robin (neighbouring stages stream from different CUs at once, which keeps
-        // HBM busier than one contiguous range per work-group), at least 2 stages and at most DEC_WG work-groups
-        // per kv head
-        const int s0 = start / KPS_F16 * KPS_F16;
-        const int nu = (kend - s0 + KPS_F16 - 1) / KPS_F16;
-        int g = nu / 2;
-        g = g < 1 ? 1 : g > DEC_WG ? DEC_WG : g;
-        return DecodePlan{0, g, 0, s0, nu};
-    }
-    // chunks of at least 128 positions, at most 124 per kv head: 248 work-groups on the 256 CUs, one each. (Measured
-    // at 64K positions: 124 chunks of 512 or 544 positions beat 128, 120 and 112 -- the work-group with the most
-    // 64-position stages sets the time.)
-    int nch = kend / 128;
-    nch = nch < 1 ? 1 : nch > 124 ? 124 : nch;
-    // boundaries planned over kend + half a chunk: the last chunk, whose work-group also writes the appended rows
-    // (mkv_append_decode), is about half as long as the others and does not finish last
-    const int span = kend + kend / (2 * nch);
-    int c0, c1;
-    chunk_range(start, kend, span, nch, c0, c1);
-    return DecodePlan{span, nch, c0};
+    const int s0 = start / KPS_F16 * KPS_F16;
+    const int nu = (kend - s0 + KPS_F16 - 1) / KPS_F16;
+    int g = nu / 2;
+    g = g < 1 ? 1 : g > DEC_WG ? DEC_WG : g;
+    return DecodePlan{0, g, 0, s0, nu};
 }
 
 hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float* q, int ntok, int n, int start,
@@ -689,13 +577,9 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
     void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
     void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
     const float scale2 = scale * LOG2E;
-    dim3 grid(p.nch - p.c0, KVH);
-    if (g.fmt == 0)
-        return launch(decode_f16<DEC_NSET>, grid, dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.s0, p.nu,
-                      ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
-    if (fa.ntok) return hipErrorNotSupported;
-    return launch(decode_f32, grid, dim3(256), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2, p.span, p.nch, p.c0,
-                  ws.part);
+    if (g.fmt != 0) return hipErrorNotSupported;
+    return launch(decode_f16<DEC_NSET>, dim3(p.nch, KVH), dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2,
+                  p.s0, p.nu, ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
 }
 
 hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,

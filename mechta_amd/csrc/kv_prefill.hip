@@ -42,7 +42,6 @@ constexpr int SLOT_BYTES = 2 * SUB * TILE_BYTES;  // K blocks, then V groups of 
 #endif
 constexpr int NSLOT = MKV_PF_NSLOT;           // LDS ring slots: NSLOT - 1 tiles in flight while one is computed
 constexpr int WGS_PER_CU = MKV_PF_WGS_PER_CU;  // work-groups the plan places per CU
-constexpr int NXCD = 8;                        // accelerator dies (XCDs) of the MI355X, each with its own L2
 
 constexpr int LPT = 2 * SUB * TILE_BYTES / NW / 1024;  // direct loads per slot and wave
 static_assert(NSLOT == 2 || LPT == 4 || LPT == 8, "wait counts below");

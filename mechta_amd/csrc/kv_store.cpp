@@ -74,13 +74,41 @@ hipError_t traced(mkv_store* h, int kind, F&& fn) {
 
 hipError_t decode_all(mkv_store* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
                       const float* gate, const FusedAppend& fa = FusedAppend{}) {
-    DecodePlan p = decode_plan(h->g.fmt, n, ntok, start);
+    if (h->g.fmt == MKV_F32) {
+        const Attn32Plan p = attn32_plan(ntok, n, start);
+        if (p.nch > h->dws.max_chunks) return hipErrorInvalidValue;
+        hipError_t e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
+            return launch_attn_f32(h->g, h->base, layer, q, ntok, n, start, scale, p, ROWS, h->dws.part, L);
+        });
+        if (e != hipSuccess) return e;
+        return traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {
+            return launch_merge(h->dws.part, ROWS, ntok, n, start, p.span, p.nch, gate, out, L);
+        });
+    }
+    DecodePlan p = decode_plan(n, ntok, start);
     hipError_t e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
         return launch_decode_core(h->g, h->base, layer, q, ntok, n, start, scale, p, h->dws, fa, L);
     });
     if (e != hipSuccess) return e;
     return traced(h, MKV_SPAN_MERGE,
                   [&](const Launch& L) { return launch_decode_merge(ntok, n, start, p, h->dws, gate, out, L); });
+}
+
+// Grows the prefill partials to `floats` (kept for later calls); false if the allocation fails.
+bool prefill_ws(mkv_store* h, size_t floats, hipError_t& e) {
+    if (floats <= h->pws_floats) return true;
+    e = hipStreamSynchronize(h->stream);
+    if (e == hipSuccess && h->pws) e = hipFree(h->pws);
+    h->pws = nullptr;
+    h->pws_floats = 0;
+    if (e == hipSuccess) e = hipMalloc(&h->pws, floats * sizeof(float));
+    if (e != hipSuccess) {
+        h->pws = nullptr;
+        (void)hipGetLastError();
+        return false;
+    }
+    h->pws_floats = floats;
+    return true;
 }
 
 void free_events(mkv_store* h) {
@@ -278,19 +306,8 @@ int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, fl
     if (h->g.fmt == MKV_F16) {
         const PrefillPlan p = prefill_plan(T, n);
         const size_t need = prefill_ws_floats(T, p.nch);
-        if (need > h->pws_floats) {  // partials of the largest prefill so far; grown on demand
-            e = hipStreamSynchronize(h->stream);
-            if (e == hipSuccess && h->pws) e = hipFree(h->pws);
-            h->pws = nullptr;
-            h->pws_floats = 0;
-            if (e == hipSuccess) e = hipMalloc(&h->pws, need * sizeof(float));
-            if (e != hipSuccess) {
-                h->pws = nullptr;
-                (void)hipGetLastError();
-                return fail(MKV_E_NOMEM, "mkv_prefill: %zu bytes of split-K partials", need * sizeof(float));
-            }
-            h->pws_floats = need;
-        }
+        if (!prefill_ws(h, need, e))
+            return fail(MKV_E_NOMEM, "mkv_prefill: %zu bytes of split-K partials", need * sizeof(float));
         e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
             return launch_prefill(h->g, h->base, layer, q, T, n, start, scale, p, h->pws, L);
         });
@@ -299,30 +316,32 @@ int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, fl
                 return launch_merge(h->pws, T * GQA, T, n, start, p.span, p.nch, gate, out, L);
             });
     } else {
-        // f32 store: exact f32 attention of the decode kernel, 4 tokens per launch (each token's causal window)
-        for (int t0 = 0; t0 < T && e == hipSuccess; t0 += 4) {
-            int nt = T - t0 < 4 ? T - t0 : 4;
-            e = decode_all(h, layer, q + (size_t)t0 * QH * HD, nt, n + t0, start, scale, out + (size_t)t0 * QH * HD,
-                           gate ? gate + (size_t)t0 * QH * 512 : nullptr);
-        }
+        // f32 store: the fp32 matrix-core kernel over blocks of 4 tokens, each token's causal window
+        const Attn32Plan p = attn32_plan(T, n, start);
+        const size_t need = prefill_ws_floats(T, p.nch);
+        if (!prefill_ws(h, need, e))
+            return fail(MKV_E_NOMEM, "mkv_prefill: %zu bytes of split-K partials", need * sizeof(float));
+        e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
+            return launch_attn_f32(h->g, h->base, layer, q, T, n, start, scale, p, T * GQA, h->pws, L);
+        });
+        if (e == hipSuccess)
+            e = traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {
+                return launch_merge(h->pws, T * GQA, T, n, start, p.span, p.nch, gate, out, L);
+            });
     }
     return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_prefill");
 }
 
-size_t mkv_snapshot_bytes(const mkv_t* h, int p) {
-    if (!h || p < 0 || p > h->g.ctx) return 0;
-    if (h->g.fmt == MKV_F32) return (size_t)h->g.layers * 2 * KVH * (size_t)p * HD * 4;
-    // f16: K planes in whole blocks of 32 positions, V planes in groups of 8 (the store's own layout)
-    size_t kb = (size_t)((p + KBLK - 1) / KBLK) * KBLK * HD * 2;
-    size_t vb = (size_t)((p + VGRP - 1) / VGRP) * VGRP * HD * 2;
-    return (size_t)h->g.layers * KVH * (kb + vb);
+// Bytes of the [0, p) prefix of one plane of K (which = 0) or V (which = 1): whole layout units (K blocks of 32
+// positions, V groups of 8 (f16) or 4 (f32) positions) of the store's own layout.
+static size_t prefix_bytes(const mkv_t* h, int which, int p) {
+    const int unit = plane_unit(h->g.fmt, which);
+    return (size_t)((p + unit - 1) / unit) * unit * HD * h->g.bpe();
 }
 
-// Bytes of the [0, p) prefix of one plane of K (which = 0) or V (which = 1).
-static size_t prefix_bytes(const mkv_t* h, int which, int p) {
-    if (h->g.fmt == MKV_F32) return (size_t)p * HD * 4;
-    int unit = which == 0 ? KBLK : VGRP;
-    return (size_t)((p + unit - 1) / unit) * unit * HD * 2;
+size_t mkv_snapshot_bytes(const mkv_t* h, int p) {
+    if (!h || p < 0 || p > h->g.ctx) return 0;
+    return (size_t)h->g.layers * KVH * (prefix_bytes(h, 0, p) + prefix_bytes(h, 1, p));
 }
 
 static int snap_copy(mkv_t* h, int p, void* host, const void* chost, size_t bytes, bool save) {

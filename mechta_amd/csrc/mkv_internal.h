@@ -15,6 +15,8 @@ constexpr int HD = 256;      // head_dim
 constexpr int GQA = QH / KVH;
 constexpr int KBLK = 32;     // K plane: positions per block, [pos/32][d/8][pos%32][8]
 constexpr int VGRP = 8;      // V plane: positions per group, [pos/8][d][pos%8]
+constexpr int VGRP32 = 4;    // f32 V plane: positions per group, [pos/4][d][pos%4]
+constexpr int NXCD = 8;      // accelerator dies (XCDs) of the MI355X, each with its own L2
 constexpr int ROWS = 32;     // query rows per KV head in decode: 4 tokens x 8 heads
 constexpr int PART = 4 + HD; // split-K partial: [m, l, 0, 0, acc[256]] (acc 16-byte aligned)
 constexpr int PACC = 4;      // offset of acc in a partial
@@ -28,6 +30,17 @@ __host__ __device__ inline size_t k_off(int pos, int d) {
 __host__ __device__ inline size_t v_off(int pos, int d) {
     return (size_t)(pos / VGRP) * (VGRP * HD) + (size_t)d * VGRP + (pos % VGRP);
 }
+
+// Element offset of (pos, d) inside one f32 K plane: [pos/32][d/4][pos%32][4].
+__host__ __device__ inline size_t k_off32(int pos, int d) {
+    return (size_t)(pos / KBLK) * (KBLK * HD) + (size_t)(d / 4) * (KBLK * 4) + (size_t)(pos % KBLK) * 4 + (d % 4);
+}
+// Element offset of (pos, d) inside one f32 V plane: [pos/4][d][pos%4].
+__host__ __device__ inline size_t v_off32(int pos, int d) {
+    return (size_t)(pos / VGRP32) * (VGRP32 * HD) + (size_t)d * VGRP32 + (pos % VGRP32);
+}
+// Positions per layout unit of a plane: K blocks of 32 in both formats, V groups of 8 (f16) or 4 (f32).
+__host__ __device__ inline int plane_unit(int fmt, int which) { return which == 0 ? KBLK : fmt == 0 ? VGRP : VGRP32; }
 
 // f32 -> f16 bits: v_cvt_f16_f32 rounds to nearest even and keeps subnormals.
 __device__ inline unsigned short f2h(float x) {
@@ -125,15 +138,13 @@ hipError_t launch_read_rows(const Geom& g, const void* base, int layer, int whic
                             const Launch& L);
 hipError_t launch_write_rows(const Geom& g, void* base, int layer, int which, int p0, int p1, const void* src,
                              const Launch& L);
-// Split-K pass and merge of the decode (two kernels).
-// f32 store: contiguous chunks of [0, span) (chunk_lo), chunks below c0 end before `start`.
-// f16 store: span = 0, c0 = 0 and the keys [s0, kend) are nu stages of KPS_F16 positions (s0 = start rounded down to
+// Split-K pass and merge of the decode on the f16 store (two kernels): span = 0, c0 = 0 and the keys [s0, kend) are nu stages of KPS_F16 positions (s0 = start rounded down to
 // a stage), dealt round robin to nch work-groups, the partial round first.
 constexpr int KPS_F16 = 64;
 struct DecodePlan {
     int span, nch, c0, s0, nu;
 };
-DecodePlan decode_plan(int fmt, int n, int ntok, int start);
+DecodePlan decode_plan(int n, int ntok, int start);
 hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float* q, int ntok, int n, int start,
                               float scale, const DecodePlan& p, const DecodeWs& ws, const FusedAppend& fa,
                               const Launch& L);
@@ -146,6 +157,14 @@ hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, 
 // q/k producer (rmsnorm of the q and k heads, rope2 of q) of ntok tokens; tab: [ntok][64] device RoPE rows.
 hipError_t launch_qk_produce(int ntok, const float* qf, const float* kb, const float* q_w, const float* k_w,
                              float eps, const float* tab, float* q_out, float* kn_out, const Launch& L);
+// Attention over the f32 store (kv_attn32.hip), decode (T <= 4) and prefill alike: nrb blocks of 4 tokens, splits
+// [c0, nch) of [0, span) (chunk_lo); partials [kvh][row < rpk][nch][PART], then launch_merge.
+struct Attn32Plan {
+    int span, nch, c0, nrb;
+};
+Attn32Plan attn32_plan(int T, int n, int start);
+hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
+                           float scale, const Attn32Plan& p, int rpk, float* part, const Launch& L);
 // Prefill (f16 store): split-K pass into the partials ws, then launch_merge with the returned plan.
 struct PrefillPlan {
     int span, nch;  // splits of [0, span) as chunk_lo

@@ -176,7 +176,8 @@ def test_decode_f16(torch_gpu, mk, ctx, n0, ntok, start):
 
 
 @pytest.mark.parametrize("ctx,n0,ntok,start", [(4096, 300, 4, 0), (4096, 1000, 1, 0), (8192, 5000, 4, 17),
-                                               (4096, 2, 1, 0)])
+                                               (4096, 2, 1, 0), (4096, 129, 2, 0), (20480, 19000, 3, 0),
+                                               (20480, 19001, 4, 12345), (8192, 40, 4, 33)])
 def test_decode_f32(torch_gpu, mk, ctx, n0, ntok, start):
     torch = torch_gpu
     print(f"decode f32 ctx={ctx} n0={n0} ntok={ntok}", flush=True)
@@ -240,16 +241,46 @@ def test_prefill_f16(torch_gpu, mk, n0, T, start):
     assert_attn_close(out, ref, what="prefill vs attn_fa_mx")
 
 
-def test_prefill_f32(torch_gpu, mk):
+@pytest.mark.parametrize("n0,T,start", [(1500, 70, 0), (100, 512, 0), (2500, 96, 300), (1, 16, 0), (3000, 5, 0),
+                                        (40, 3, 0), (3500, 512, 2900)])
+def test_prefill_f32(torch_gpu, mk, n0, T, start):
     torch = torch_gpu
-    n0, T = 1500, 70
+    print(f"prefill f32 n0={n0} T={T} start={start}", flush=True)
     with mk.KvStore(1, 4096, F32) as st:
-        fill(torch, st, 0, F32, n0 + T - 1, seed=700)
-        q = q_inputs(701, T)
-        out = st.prefill(0, dev(torch, q), n0).cpu().numpy()
+        fill(torch, st, 0, F32, n0 + T - 1, seed=700 + T)
+        q = q_inputs(701 + T, T)
+        out = st.prefill(0, dev(torch, q), n0, start=start).cpu().numpy()
         kc, vc = caches_np(st, 0, n0 + T - 1)
-    ref = O.attn_fa_f32(kc, vc, q, n0)
+    ref = O.attn_fa_f32(kc, vc, q, n0, start=start)
     assert_attn_close(out, ref, atol=1e-5, rtol=1e-5, what="prefill f32")
+
+
+@pytest.mark.parametrize("fmt", [F16, F32])
+def test_stale_nan_rows_past_the_length(torch_gpu, mk, fmt):
+    """Rows past the written length (rejected drafts, never-written memory) may hold anything, NaN included: decode
+    and prefill read whole blocks and must keep those rows out of the results."""
+    torch = torch_gpu
+    n0, ntok, T = 1000, 4, 40
+    with mk.KvStore(1, 4096, fmt) as st:
+        fill(torch, st, 0, fmt, n0 + 100, seed=41)
+        nan = torch.full((102 - ntok, 2, 256), float("nan"), device="cuda")
+        if fmt == F16:
+            nan = nan.half().view(torch.int16)
+        for which in (0, 1):
+            st.write_rows(0, which, n0 + ntok - 1, n0 + 101, nan)
+        st.set_len(n0 + ntok - 1)
+        q = q_inputs(42, ntok)
+        out = st.decode(0, dev(torch, q), n0).cpu().numpy()
+        qp = q_inputs(43, T)
+        outp = st.prefill(0, dev(torch, qp), n0 + ntok - T).cpu().numpy()
+        kc, vc = caches_np(st, 0, n0 + ntok - 1)
+    if fmt == F16:
+        assert_attn_close(out, O.attn_dmx(kc, vc, q, n0), what="decode next to NaN rows")
+        assert_attn_close(outp, O.attn_fa_mx(kc, vc, qp, n0 + ntok - T), what="prefill next to NaN rows")
+    else:
+        assert_attn_close(out, O.attn_fd(F32, kc, vc, q, n0), atol=1e-5, rtol=1e-5, what="decode next to NaN rows")
+        assert_attn_close(outp, O.attn_fa_f32(kc, vc, qp, n0 + ntok - T), atol=1e-5, rtol=1e-5,
+                          what="prefill next to NaN rows")
 
 
 # ------------------------------------------------------------------------------------------------ snapshot -------
