@@ -3,7 +3,9 @@
 // prefill (attn_fa, ops.wgsl:540-651), one kernel for both.
 //
 // Work-group (block of 4 tokens, key split, kv head): 32 query rows (token * 8 + head) against the split's keys in
-// tiles of 32 keys, 4 waves. Per tile, wave w
+// tiles of 32 keys, by NWG groups of 4 waves that take alternate tiles. Prefill runs two groups (two waves per SIMD:
+// one group's MFMAs run while the other waits for its loads; their states are merged through LDS at the end). Decode
+// runs one: its splits are only 4-5 tiles long, too few to share. Per tile, wave w of a group
 //   S^T[32 keys][32 rows] over dims 64w .. 64w+63    32 x v_mfma_f32_32x32x2_f32, A = K straight from HBM, B = Q (LDS)
 //   the four partial S^T summed through LDS ((w0 + w1) + (w2 + w3), the same order in every wave)
 //   exact-max online softmax of the 32 rows (each wave redundantly: 16 scores per lane)
@@ -34,7 +36,8 @@ struct Tile {
     f32x4 v[8];  // V: keys 8q + 4s .. +3 of dim 64w + 32c + l % 32 (index 4c + q)
 };
 
-__global__ void __launch_bounds__(256) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
+template <int NWG>  // wave groups
+__global__ void __launch_bounds__(256 * NWG) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
                                                 size_t plane_elems, const float* __restrict__ q, int T, int n,
                                                 int start, float scale2, int span, int nch, int c0, int nrb, int rpk,
                                                 float* __restrict__ part) {
@@ -44,7 +47,7 @@ __global__ void __launch_bounds__(256) attn_f32(const float* __restrict__ kplane
     const int W = G % NXCD == 0 ? (L % NXCD) * (G / NXCD) + L / NXCD : L;
     const int ncg = nch - c0;
     const int rb = W % nrb, c = c0 + (W / nrb) % ncg, kvh = W / nrb / ncg;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, s = lane >> 5, r32 = lane & 31;
+    const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 8, w = (tid >> 6) & 3, s = lane >> 5, r32 = lane & 31;
     const int t0 = 4 * rb, nt = min(4, T - t0);
     const int kend = n + T - 1;  // keys of the whole call
     const int cs = chunk_lo(c, span, nch), ce = c + 1 < nch ? chunk_lo(c + 1, span, nch) : kend;
@@ -52,8 +55,8 @@ __global__ void __launch_bounds__(256) attn_f32(const float* __restrict__ kplane
     const int ntile = hi > lo ? (hi - lo + TILE - 1) / TILE : 0;
 
     __shared__ float qs[ROWS][QPAD];
-    __shared__ f32x4 sx[2][4][4][64];  // partial S^T: [tile parity][wave][register quad][lane]
-    for (int i = tid; i < ROWS * HD / 4; i += 256) {
+    __shared__ f32x4 sx[2][NWG][4][4][64];  // partial S^T: [tile parity][group][wave][register quad][lane]
+    for (int i = tid; i < ROWS * HD / 4; i += 256 * NWG) {
         const int row = i / (HD / 4), d4 = (i % (HD / 4)) * 4, t = t0 + (row >> 3);
         f32x4 x = f32x4{};
         if (t < T) x = *(const f32x4*)(q + ((size_t)t * QH + kvh * GQA + (row & 7)) * HD + d4);
@@ -77,7 +80,7 @@ __global__ void __launch_bounds__(256) attn_f32(const float* __restrict__ kplane
             X.v[cq] = bload4f(vr, base + vofs + (cq & 3) * (2 * 4 * HD * 4) + (cq >> 2) * (32 * 4 * 4));
     };
 
-    const int vis = n + t0 + (r32 >> 3);  // lane's row sees keys < vis
+    const int vis = n + t0 + (r32 >> 3);  // lane's row sees keys < vis (and of this split, < hi)
     float m_run = NEG_INF, l_run = 0.f;
     f32x16 O[2] = {f32x16{}, f32x16{}};
     auto step = [&](Tile& X, int j) {
@@ -89,15 +92,16 @@ __global__ void __launch_bounds__(256) attn_f32(const float* __restrict__ kplane
 #pragma unroll
             for (int b = 0; b < 4; b++) S = mfma32f(X.k[m][b], qv[b], S);
         }
-        const int pb = j & 1;
+        const int pb = (j / NWG) & 1;
+        f32x4(&sg)[4][4][64] = sx[pb][grp];
 #pragma unroll
-        for (int a = 0; a < 4; a++) sx[pb][w][a][lane] = f32x4{S[4 * a], S[4 * a + 1], S[4 * a + 2], S[4 * a + 3]};
-        lds_barrier();  // parity buffers: tile j + 2 writes pb again only after every wave passed tile j + 1's barrier
+        for (int a = 0; a < 4; a++) sg[w][a][lane] = f32x4{S[4 * a], S[4 * a + 1], S[4 * a + 2], S[4 * a + 3]};
+        lds_barrier();  // parity buffers: a group's round i + 2 writes pb again only after every wave passed round i + 1
         float sv[16];
 #pragma unroll
         for (int a = 0; a < 4; a++) {
-            const f32x4 p0 = sx[pb][0][a][lane], p1 = sx[pb][1][a][lane];
-            const f32x4 p2 = sx[pb][2][a][lane], p3 = sx[pb][3][a][lane];
+            const f32x4 p0 = sg[0][a][lane], p1 = sg[1][a][lane];
+            const f32x4 p2 = sg[2][a][lane], p3 = sg[3][a][lane];
 #pragma unroll
             for (int b = 0; b < 4; b++) sv[4 * a + b] = (p0[b] + p1[b]) + (p2[b] + p3[b]);
         }
@@ -106,7 +110,7 @@ __global__ void __launch_bounds__(256) attn_f32(const float* __restrict__ kplane
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int key = k0 + 8 * (i >> 2) + 4 * s + (i & 3);
-            sv[i] = (key >= start && key < vis) ? sv[i] * scale2 : NEG_INF;
+            sv[i] = (key >= start && key < vis && key < hi) ? sv[i] * scale2 : NEG_INF;
             mt = fmaxf(mt, sv[i]);
         }
         mt = fmaxf(mt, __shfl_xor(mt, 32));
@@ -147,14 +151,51 @@ __global__ void __launch_bounds__(256) attn_f32(const float* __restrict__ kplane
                 for (int b = 0; b < 4; b++) O[cc] = mfma32f(sv[4 * qq + b], X.v[4 * cc + qq][b], O[cc]);
     };
 
+    // group g takes tiles g, g + 2, ...; both run the same number of rounds (every wave meets every barrier): a round
+    // past the last tile loads nothing (zeros) and has every key masked
+    const int rounds = (ntile + NWG - 1) / NWG;
     Tile A, B;
-    load(A, 0);
-    for (int j = 0; j < ntile; j += 2) {
-        load(B, j + 1);
-        step(A, j);
-        if (j + 1 >= ntile) break;
-        load(A, j + 2);
-        step(B, j + 1);
+    load(A, grp);
+    for (int i = 0; i < rounds; i += 2) {
+        load(B, (i + 1) * NWG + grp);
+        step(A, i * NWG + grp);
+        if (i + 1 >= rounds) break;
+        load(A, (i + 2) * NWG + grp);
+        step(B, (i + 1) * NWG + grp);
+    }
+
+    // merge group 1 into group 0 through LDS (the parity buffers are free after the barrier)
+    if constexpr (NWG == 2) {
+        __syncthreads();
+        float* ob = (float*)&sx[0][0][0][0][0];  // [wave][2][16][64] O of group 1, then m, l of its 32 rows
+        float* ml = ob + 4 * 2 * 16 * 64;
+        if (grp == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                ob[((w * 2 + 0) * 16 + i) * 64 + lane] = O[0][i];
+                ob[((w * 2 + 1) * 16 + i) * 64 + lane] = O[1][i];
+            }
+            if (w == 0 && s == 0) {
+                ml[r32] = m_run;
+                ml[32 + r32] = l_run;
+            }
+        }
+        __syncthreads();
+        if (grp == 1) return;
+        {
+            const float m1 = ml[r32], l1 = ml[32 + r32];
+            const float M = fmaxf(m_run, m1);
+            const float f0 = m_run == NEG_INF ? 0.f : exp2f(m_run - M), f1 = m1 == NEG_INF ? 0.f : exp2f(m1 - M);
+            l_run = l_run * f0 + l1 * f1;
+            m_run = M;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int row = 8 * (i >> 2) + 4 * s + (i & 3);
+                const float g0 = __shfl(f0, row), g1 = __shfl(f1, row);
+                O[0][i] = O[0][i] * g0 + ob[((w * 2 + 0) * 16 + i) * 64 + lane] * g1;
+                O[1][i] = O[1][i] * g0 + ob[((w * 2 + 1) * 16 + i) * 64 + lane] * g1;
+            }
+        }
     }
 
     // partials of the rows of present tokens: [kvh][row < rpk][chunk < nch][PART], row = token * 8 + head
@@ -204,8 +245,11 @@ hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const flo
     const float* kp = (const float*)(b + g.plane(layer, 0, 0) * g.plane_bytes());
     const float* vp = (const float*)(b + g.plane(layer, 1, 0) * g.plane_bytes());
     dim3 grid(p.nrb * (p.nch - p.c0) * KVH);
-    return launch(attn_f32, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span, p.nch,
-                  p.c0, p.nrb, rpk, part);
+    if (T <= 4)
+        return launch(attn_f32<1>, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
+                      p.nch, p.c0, p.nrb, rpk, part);
+    return launch(attn_f32<2>, grid, dim3(512), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
+                  p.nch, p.c0, p.nrb, rpk, part);
 }
 
 }  // namespace mkv
