@@ -269,6 +269,61 @@ def bench_cfg4(torch, mk, positions):
     return us, keys * 2048 / (positions - 1) / (us * 1e-6) / 1e9
 
 
+def bench_cfg5(torch, mk, reps=3):
+    """f32 store, 10 layers x 16,384 positions (671 MB): snapshot to pinned host memory, restore
+    into a fresh store, then a 4-token verify per layer, checked bit-identical to the same verify before the
+    snapshot. Returns the snapshot and restore rates (host link), the verify's µs per layer and the identity flag."""
+    L, N0, NT = 10, 16384, 4
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2032)
+    tabs = rope_tabs(torch, mk, 0, N0)
+    a = mk.KvStore(L, 17408, mk.F32)
+    for layer in range(L):
+        fill_store(torch, mk, a, layer, N0 - NT + 1, gen, tabs)
+    kn, v = seeded_normal(torch, gen, (NT, 2, 256)), seeded_normal(torch, gen, (NT, 512))
+    q = seeded_normal(torch, gen, (NT, 16, 256))
+    p = N0 - NT + 1
+    nb = a.snapshot_bytes(p)
+    host = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+
+    def verify(st):
+        outs = []
+        for layer in range(L):
+            outs.append(st.append_decode(layer, p, kn, v, tabs[p - 1:p - 1 + NT], q))
+            st.set_len(p)
+        return outs
+
+    before = verify(a)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        a.snapshot(p, host)
+    t_snap = (time.perf_counter() - t0) / reps
+    a.close()
+    b = mk.KvStore(L, 17408, mk.F32)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        b.restore(p, host)
+        b.sync()
+    t_rest = (time.perf_counter() - t0) / reps
+    after = verify(b)
+    same = all(torch.equal(x, y) for x, y in zip(before, after))
+    for _ in range(3):
+        verify(b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        verify(b)
+    e1.record()
+    torch.cuda.synchronize()
+    b.close()
+    return dict(snapshot_gbps=round(nb / t_snap / 1e9, 2), restore_gbps=round(nb / t_rest / 1e9, 2),
+                snapshot_mb=round(nb / 1e6, 1), verify_us_per_layer=round(e0.elapsed_time(e1) / (10 * L) * 1000, 2),
+                bit_identical=bool(same))
+
+
 def cpu_baseline(dec, budget_s):
     """The oracle's attn_dmx + append on the bench's own cache, on this host's cores."""
     import numpy as np
@@ -351,6 +406,7 @@ def main():
         us4, gbs4 = bench_cfg4(torch, mk, 20)
         res["cfg4_us_per_position_10_layers"] = round(us4, 1)
         res["cfg4_kv_read_gbps"] = round(gbs4, 1)
+        res["cfg5"] = bench_cfg5(torch, mk)
     if args.calib_copy:
         # plain elementwise copy of a known size: its FETCH_SIZE / WRITE_SIZE counters give the scale from counter
         # units to bytes for the KV kernels' counters in the same run
