@@ -50,7 +50,6 @@ __device__ inline float reduce16(float x, Op op) {
 // access, which masks lanes or whole loads without a branch (and so without the waits a branch around a load makes
 // the compiler insert).
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr unsigned OOB = 0xFFFFFF00u;  // an offset past every plane
 // base and bytes must be wave-uniform; they are read from the first lane so that the resource lives in scalar
 // registers (a resource in vector registers makes the compiler loop over lanes around every load)
 __device__ inline rsrc_t plane_rsrc(const void* base, unsigned bytes) {

@@ -41,6 +41,11 @@ def lib():
         _lib.orc_rmsnorm_rows.argtypes = [P, I, I, P, F, P]
         _lib.orc_qk_norm_rope.argtypes = [P, P, I, P, P, F, P, P, P]
         _lib.orc_threads.restype = I
+        _lib.orc_fl_rope_table.argtypes = [I, F, P]
+        _lib.orc_fl_rope.argtypes = [I, I, P, P, P]
+        _lib.orc_fl_kv_write.argtypes = [I, P, P, I, I, I, P, P]
+        _lib.orc_fl_attn_fd.argtypes = [I, P, P, I, P, I, I, P, P]
+        _lib.orc_fl_attn_pf.argtypes = [I, P, P, I, P, I, I, I, P, P]
     return _lib
 
 
@@ -165,3 +170,65 @@ def qk_norm_rope(qf, kb, q_w, k_w, tab, eps=1e-6):
 
 def threads():
     return lib().orc_threads()
+
+
+# ---------------------------------------------------------------- Flint (flint_oracle.c) ----------------------------
+# Flint caches: [ring][4 kvh][128] per layer (row = position % ring), f32 or f16 bit patterns.
+FL_H, FL_KVH, FL_D = 32, 4, 128
+FL_WINDOW, FL_RING = 513, 1024
+
+
+def _pp(a):
+    return None if a is None else _p(a)
+
+
+def fl_rope_table(pos, base=10000.0):
+    t = np.empty(FL_D, np.float32)
+    lib().orc_fl_rope_table(pos, base, _p(t))
+    return t
+
+
+def fl_rope_tables(pos0, ntok, base=10000.0):
+    return np.stack([fl_rope_table(pos0 + t, base) for t in range(ntok)])
+
+
+def fl_rope(x, tabs):
+    x = _c(x, np.float32)
+    ntok = tabs.shape[0]
+    heads = x.size // (ntok * FL_D)
+    out = np.empty_like(x)
+    lib().orc_fl_rope(ntok, heads, _p(x), _p(_c(tabs, np.float32)), _p(out))
+    return out
+
+
+def fl_new_cache(rows, fmt):
+    return np.zeros((rows, FL_KVH, FL_D), np.uint16 if fmt == 0 else np.float32)
+
+
+def fl_kv_write(fmt, kc, vc, pos0, k, v):
+    k, v = _c(k, np.float32), _c(v, np.float32)
+    n = k.size // (FL_KVH * FL_D)
+    lib().orc_fl_kv_write(fmt, _p(kc), _p(vc), kc.shape[0], pos0, n, _p(k), _p(v))
+
+
+def fl_window_lo(pos, win):
+    return pos + 1 - win if win and pos + 1 > win else 0
+
+
+def fl_attn_fd(fmt, kc, vc, q, pos, win, sinks):
+    """One token at position `pos`: positions [lo, pos] as attn_fd + attn_fd_merge."""
+    q = _c(q, np.float32)
+    lo = fl_window_lo(pos, win)
+    out = np.empty((FL_H, FL_D), np.float32)
+    s = None if sinks is None else _c(sinks, np.float32)
+    lib().orc_fl_attn_fd(fmt, _p(kc), _p(vc), kc.shape[0], _p(q), lo, pos + 1 - lo, _pp(s), _p(out))
+    return out
+
+
+def fl_attn_pf(fmt, kc, vc, q, pos0, win, sinks):
+    """Block of n tokens at pos0 .. pos0 + n - 1 as attn_pf."""
+    q = _c(q, np.float32).reshape(-1, FL_H, FL_D)
+    out = np.empty_like(q)
+    s = None if sinks is None else _c(sinks, np.float32)
+    lib().orc_fl_attn_pf(fmt, _p(kc), _p(vc), kc.shape[0], _p(q), pos0, q.shape[0], win, _pp(s), _p(out))
+    return out
