@@ -22,6 +22,16 @@ namespace {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
+#ifndef FL_DEC_BUF
+#define FL_DEC_BUF 2      // decode: subtiles in registers per wave
+#endif
+#ifndef FL_DEC_SPLIT
+#define FL_DEC_SPLIT 32   // decode: positions per split at least
+#endif
+#ifndef FL_DEC_NCH
+#define FL_DEC_NCH 64     // decode: splits per kv head at most
+#endif
+
 constexpr int TILE = 32;
 constexpr int QPAD = HD + 4;  // LDS row of Q (floats)
 
@@ -45,7 +55,7 @@ struct TileRegs<0> {  // f16: K dims 32w + 16a + 8s .. +7 (a < 2); V as f32, 4 h
     half4 v[4];
 };
 
-template <int FMT, int NWG>
+template <int FMT, int NWG, int NBUF>  // NBUF: tiles in registers (NBUF - 1 in flight ahead of the one computed)
 __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kplane, const void* __restrict__ vplane,
                                                      size_t plane_elems, int rows, const float* __restrict__ q, int T,
                                                      int pos0, int win, float scale2, int klo, int span, int nch,
@@ -185,15 +195,20 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
             for (int b = 0; b < 4; b++) O = mfma32f(sv[4 * qq + b], vv[qq][b], O);
     };
 
+    // a ring of NBUF register tiles: round r computes slot r % NBUF after issuing the loads of round r + NBUF - 1
+    // into the slot round r - 1 freed (the slots are unrolled, so every index is a constant)
     const int rounds = (ntile + NWG - 1) / NWG;
-    TileRegs<FMT> A, B;
-    load(A, grp);
-    for (int i = 0; i < rounds; i += 2) {
-        load(B, (i + 1) * NWG + grp);
-        step(A, i * NWG + grp);
-        if (i + 1 >= rounds) break;
-        load(A, (i + 2) * NWG + grp);
-        step(B, (i + 1) * NWG + grp);
+    TileRegs<FMT> R[NBUF];
+#pragma unroll
+    for (int k = 0; k < NBUF - 1; k++) load(R[k], k * NWG + grp);
+    for (int i0 = 0; i0 < rounds; i0 += NBUF) {
+#pragma unroll
+        for (int k = 0; k < NBUF; k++) {
+            if (i0 + k < rounds) {  // uniform in the work-group
+                load(R[(k + NBUF - 1) % NBUF], (i0 + k + NBUF - 1) * NWG + grp);
+                step(R[k], (i0 + k) * NWG + grp);
+            }
+        }
     }
 
     if constexpr (NWG == 2) {  // group 1's state into group 0 through LDS
@@ -237,28 +252,62 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
 }
 
 // Merge of the splits with the sink (attn_fd_merge, flint_attn.wgsl:241-257): M = max(sink, m_c), out =
-// sum_c 2^(m_c - M) acc_c / (2^(sink - M) + sum_c 2^(m_c - M) l_c), all in log2 units. 8 rows (token, head) per
-// work-group of 256 threads, 4 dims per thread.
+// sum_c 2^(m_c - M) acc_c / (2^(sink - M) + sum_c 2^(m_c - M) l_c), all in log2 units. Work-group = row (token, head);
+// its 256 threads are 8 split lanes x 32 dim lanes (4 dims each): every split of the row is loaded in one round trip
+// (split lane i takes splits i, i + 8, ...), then the split lanes are combined through LDS.
+constexpr int MERGE_J = 16;  // splits per split lane: 8 x 16 >= the at most 128 splits of a plan
+
 __global__ void __launch_bounds__(256) fl_merge(const float* __restrict__ part, int T, int nch,
                                                 const float* __restrict__ sinks, float* __restrict__ out) {
-    const int rowid = blockIdx.x * 8 + (threadIdx.x >> 5);  // t * 32 + head
-    if (rowid >= T * QH) return;
-    const int t = rowid / QH, head = rowid % QH, d0 = (threadIdx.x & 31) * 4;
+    const int t = blockIdx.x / QH, head = blockIdx.x % QH, tid = threadIdx.x;
+    const int cl = tid >> 5, d0 = (tid & 31) * 4;
     const float* p = part + ((size_t)(head / GQA) * T * GQA + (size_t)t * GQA + head % GQA) * nch * PART;
-    float M = sinks ? sinks[head] * LOG2E : NEG_INF;
-    for (int c = 0; c < nch; c++) M = fmaxf(M, p[(size_t)c * PART]);
-    float Lsum = sinks && M != NEG_INF ? exp2f(sinks[head] * LOG2E - M) : 0.f;
-    f32x4 acc = f32x4{};
-#pragma unroll 4
-    for (int c = 0; c < nch; c++) {
-        const float* pc = p + (size_t)c * PART;
-        const float mc = pc[0];
-        const float e = mc == NEG_INF ? 0.f : exp2f(mc - M);
-        Lsum += e * pc[1];
-        const f32x4 a = *(const f32x4*)(pc + PACC + d0);
-        acc += e * a;
+    __shared__ float red[8];
+    __shared__ f32x4 accs[8][32];
+    __shared__ float ls[8];
+    float mj[MERGE_J], lj[MERGE_J];
+    f32x4 aj[MERGE_J];
+    float M = NEG_INF;
+#pragma unroll
+    for (int j = 0; j < MERGE_J; j++) {
+        const int c = cl + 8 * j;
+        mj[j] = NEG_INF;
+        lj[j] = 0.f;
+        aj[j] = f32x4{};
+        if (c < nch) {
+            const float* pc = p + (size_t)c * PART;
+            mj[j] = pc[0];
+            lj[j] = pc[1];
+            aj[j] = *(const f32x4*)(pc + PACC + d0);
+        }
+        M = fmaxf(M, mj[j]);
     }
-    *(f32x4*)(out + ((size_t)t * QH + head) * HD + d0) = acc / Lsum;
+    if ((tid & 31) == 0) red[cl] = M;
+    __syncthreads();
+    M = sinks ? sinks[head] * LOG2E : NEG_INF;
+#pragma unroll
+    for (int i = 0; i < 8; i++) M = fmaxf(M, red[i]);
+    f32x4 acc = f32x4{};
+    float L = 0.f;
+#pragma unroll
+    for (int j = 0; j < MERGE_J; j++) {
+        const float e = mj[j] == NEG_INF ? 0.f : exp2f(mj[j] - M);
+        L += e * lj[j];
+        acc += e * aj[j];
+    }
+    accs[cl][tid & 31] = acc;
+    if ((tid & 31) == 0) ls[cl] = L;
+    __syncthreads();
+    if (tid < 32) {
+        f32x4 sum = f32x4{};
+        float lt = sinks && M != NEG_INF ? exp2f(sinks[head] * LOG2E - M) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            sum += accs[i][tid];
+            lt += ls[i];
+        }
+        *(f32x4*)(out + ((size_t)t * QH + head) * HD + d0) = sum / lt;
+    }
 }
 
 // K and V rows of ntok tokens into ring rows (pos0 + t) % rows: items (token, kv head, 8 dims).
@@ -317,6 +366,254 @@ __global__ void __launch_bounds__(256) fl_rows(E* __restrict__ plane, size_t pla
     else plane[o] = rowsbuf[id];
 }
 
+
+// ---- one or two tokens: 16 query rows (token * 8 + head) on v_mfma_f32_16x16x4_f32 ----
+// Work-group (key split, kv head), 4 waves; each wave owns whole 16-position subtiles (w, w + 4, ...) over all 128
+// dims, so no per-tile exchange or barrier: S^T[16 keys][16 rows] is 32 MFMAs with A = K straight from HBM and B = Q
+// in registers, and P.V is 32 MFMAs with A = P (the S^T registers: lane l holds row l % 16 and keys 4g + r, g = l / 16,
+// register r) and B = V. The four waves' states are merged through LDS at the end; one partial per work-group.
+__device__ inline f32x4 mfma16f(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int FMT>
+struct SubRegs;
+template <>
+struct SubRegs<1> {  // f32: K dims 16a + 4g .. +3 of key l % 16 (a < 8); V keys 4g .. +3 of dim 16c + l % 16 (c < 8)
+    f32x4 k[8];
+    f32x4 v[8];
+};
+template <>
+struct SubRegs<0> {  // f16: K dims 32a + 8g .. +7 (a < 4); V as f32, 4 halves
+    half8 k[4];
+    half4 v[8];
+};
+
+template <int FMT, int NBUF>
+__global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane, const void* __restrict__ vplane,
+                                                size_t plane_elems, int rows, const float* __restrict__ q, int T,
+                                                int pos0, int win, float scale2, int klo, int span, int nch,
+                                                float* __restrict__ part) {
+    constexpr int BPE = FMT == 1 ? 4 : 2;
+    const int c = blockIdx.x % nch, kvh = blockIdx.x / nch;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
+    const int lo_first = window_lo(pos0, win);
+    const int cs = klo + chunk_lo(c, span, nch), ce = c + 1 < nch ? klo + chunk_lo(c + 1, span, nch) : klo + span;
+    const int lo = max(cs, lo_first / TILE * TILE), hi = min(ce, pos0 + T);
+    const int nsub = hi > lo ? (hi - lo + 15) / 16 : 0;
+
+    // Q of the lane's row in registers, in the dim order of the K operands
+    float qv[32];
+    {
+        const int t = r16 >> 3;
+        const float* qr = q + ((size_t)t * QH + kvh * GQA + (r16 & 7)) * HD;
+#pragma unroll
+        for (int a = 0; a < 32 / 4; a++) {
+            const int d = FMT == 1 ? 16 * a + 4 * g : 32 * (a >> 1) + 8 * g + 4 * (a & 1);
+            const f32x4 x = t < T ? *(const f32x4*)(qr + d) : f32x4{};
+#pragma unroll
+            for (int b = 0; b < 4; b++) qv[4 * a + b] = x[b];
+        }
+    }
+    const unsigned pbytes = (unsigned)(plane_elems * BPE);
+    const rsrc_t kr = plane_rsrc((const char*)kplane + (size_t)kvh * plane_elems * BPE, pbytes);
+    const rsrc_t vr = plane_rsrc((const char*)vplane + (size_t)kvh * plane_elems * BPE, pbytes);
+    auto load = [&](SubRegs<FMT>& X, int j) {
+        unsigned blk = pbytes;  // subtiles past the last: every offset lies past the plane (zeros)
+        int sub = 0;
+        if (j < nsub) {
+            const int r0 = (lo + 16 * j) % rows;
+            blk = (unsigned)(r0 / 32) * (32 * HD * BPE);
+            sub = r0 % 32;
+        }
+        if constexpr (FMT == 1) {
+#pragma unroll
+            for (int a = 0; a < 8; a++)
+                X.k[a] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       kr, blk + ((4 * a + g) * 32 + sub + r16) * 16, 0, 0));
+#pragma unroll
+            for (int cc = 0; cc < 8; cc++)
+                X.v[cc] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        vr, blk + ((sub / 4 + g) * HD + 16 * cc + r16) * 16, 0, 0));
+        } else {
+#pragma unroll
+            for (int a = 0; a < 4; a++) X.k[a] = bload16(kr, blk + ((4 * a + g) * 32 + sub + r16) * 16);
+            const int rr = sub + 4 * g;
+#pragma unroll
+            for (int cc = 0; cc < 8; cc++)
+                X.v[cc] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(
+                                                        vr, blk + ((rr / 8) * HD * 8 + (16 * cc + r16) * 8 + rr % 8) * 2,
+                                                        0, 0));
+        }
+    };
+
+    const int prow = pos0 + (r16 >> 3);
+    const int plo = window_lo(prow, win);
+    float m_run = NEG_INF, l_run = 0.f;
+    f32x4 O[8];
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) O[cc] = f32x4{};
+    auto step = [&](SubRegs<FMT>& X, int j) {
+        const int k0 = lo + 16 * j;
+        f32x4 S = f32x4{};
+        if constexpr (FMT == 1) {
+#pragma unroll
+            for (int a = 0; a < 8; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) S = mfma16f(X.k[a][b], qv[4 * a + b], S);
+        } else {
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 8; b++) S = mfma16f((float)X.k[a][b], qv[8 * a + b], S);
+        }
+        float sv[4];
+        float mt = NEG_INF;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int key = k0 + 4 * g + r;
+            sv[r] = (key >= plo && key <= prow && key < hi) ? S[r] * scale2 : NEG_INF;
+            mt = fmaxf(mt, sv[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m_run, mt);
+        const float base = mn == NEG_INF ? 0.f : mn;
+        const float cf = m_run == NEG_INF ? 0.f : exp2f(m_run - mn);
+        float ls = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            sv[r] = exp2f(sv[r] - base);
+            ls += sv[r];
+        }
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        l_run = l_run * cf + ls;
+        m_run = mn;
+        if (__builtin_amdgcn_ballot_w64(cf != 1.f)) {  // register r of O holds row 4g + r
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float f = __shfl(cf, 4 * g + r);
+#pragma unroll
+                for (int cc = 0; cc < 8; cc++) O[cc][r] *= f;
+            }
+        }
+        float vv[8][4];
+#pragma unroll
+        for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) vv[cc][r] = (float)X.v[cc][r];
+        if (k0 < lo_first || k0 + 16 > hi) {  // rows of other or unwritten positions: no NaN through V
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = k0 + 4 * g + r;
+                if (key < lo_first || key >= hi)
+#pragma unroll
+                    for (int cc = 0; cc < 8; cc++) vv[cc][r] = 0.f;
+            }
+        }
+#pragma unroll
+        for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) O[cc] = mfma16f(sv[r], vv[cc][r], O[cc]);
+    };
+
+    const int mine = nsub > w ? (nsub - w + 3) / 4 : 0;  // this wave's subtiles w, w + 4, ...
+    SubRegs<FMT> R[NBUF];
+#pragma unroll
+    for (int k = 0; k < NBUF - 1; k++) load(R[k], w + 4 * k);
+    for (int i0 = 0; i0 < mine; i0 += NBUF) {
+#pragma unroll
+        for (int k = 0; k < NBUF; k++) {
+            if (i0 + k < mine) {  // uniform in the wave
+                load(R[(k + NBUF - 1) % NBUF], w + 4 * (i0 + k + NBUF - 1));
+                step(R[k], w + 4 * (i0 + k));
+            }
+        }
+    }
+
+    // the four waves' states into one partial
+    __shared__ f32x4 ob[4][8][64];
+    __shared__ float ml[4][2][16];
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) ob[w][cc][lane] = O[cc];
+    if (g == 0) {
+        ml[w][0][r16] = m_run;
+        ml[w][1][r16] = l_run;
+    }
+    __syncthreads();
+    if (w != 0) return;
+    const size_t rbase = (size_t)kvh * T * GQA;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int row = 4 * g + r;
+        float M = NEG_INF;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, ml[ww][0][row]);
+        float f[4];
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) f[ww] = ml[ww][0][row] == NEG_INF ? 0.f : exp2f(ml[ww][0][row] - M);
+        if (row < T * GQA) {
+            float* p = part + ((rbase + row) * nch + c) * PART + PACC + r16;
+#pragma unroll
+            for (int cc = 0; cc < 8; cc++) {
+                float o = 0.f;
+#pragma unroll
+                for (int ww = 0; ww < 4; ww++) o += f[ww] * ob[ww][cc][lane][r];
+                p[16 * cc] = o;
+            }
+        }
+    }
+    if (g == 0 && r16 < T * GQA) {
+        float M = NEG_INF, Lt = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, ml[ww][0][r16]);
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++)
+            Lt += ml[ww][0][r16] == NEG_INF ? 0.f : exp2f(ml[ww][0][r16] - M) * ml[ww][1][r16];
+        float* p = part + ((rbase + r16) * nch + c) * PART;
+        p[0] = M;
+        p[1] = Lt;
+    }
+}
+
+// Merge for few splits (prefill blocks): 8 rows (token, head) per work-group of 256 threads, 4 dims per thread, the
+// splits of a row loaded in one round trip.
+constexpr int MERGE_FEW = 16;
+
+__global__ void __launch_bounds__(256) fl_merge_few(const float* __restrict__ part, int T, int nch,
+                                                    const float* __restrict__ sinks, float* __restrict__ out) {
+    const int rowid = blockIdx.x * 8 + (threadIdx.x >> 5);  // t * 32 + head
+    if (rowid >= T * QH) return;
+    const int t = rowid / QH, head = rowid % QH, d0 = (threadIdx.x & 31) * 4;
+    const float* p = part + ((size_t)(head / GQA) * T * GQA + (size_t)t * GQA + head % GQA) * nch * PART;
+    float mj[MERGE_FEW], lj[MERGE_FEW];
+    f32x4 aj[MERGE_FEW];
+    float M = sinks ? sinks[head] * LOG2E : NEG_INF;
+#pragma unroll
+    for (int j = 0; j < MERGE_FEW; j++) {
+        mj[j] = NEG_INF;
+        lj[j] = 0.f;
+        aj[j] = f32x4{};
+        if (j < nch) {
+            const float* pc = p + (size_t)j * PART;
+            mj[j] = pc[0];
+            lj[j] = pc[1];
+            aj[j] = *(const f32x4*)(pc + PACC + d0);
+        }
+        M = fmaxf(M, mj[j]);
+    }
+    float L = sinks && M != NEG_INF ? exp2f(sinks[head] * LOG2E - M) : 0.f;
+    f32x4 acc = f32x4{};
+#pragma unroll
+    for (int j = 0; j < MERGE_FEW; j++) {
+        const float e = mj[j] == NEG_INF ? 0.f : exp2f(mj[j] - M);
+        L += e * lj[j];
+        acc += e * aj[j];
+    }
+    *(f32x4*)(out + ((size_t)t * QH + head) * HD + d0) = acc / L;
+}
+
 }  // namespace
 
 Plan plan(int pos0, int T, int win) {
@@ -324,8 +621,11 @@ Plan plan(int pos0, int T, int win) {
     const int klo = lo0 / 32 * 32, span = pos0 + T - klo;
     const int nrb = (T + 3) / 4;
     int nch;
-    if (T <= 4) {
-        nch = span / 128;  // splits of at least 128 positions, 256 work-groups over the 4 kv heads at most
+    if (T <= 2) {  // fl_dec16
+        nch = span / FL_DEC_SPLIT;
+        nch = nch > FL_DEC_NCH ? FL_DEC_NCH : nch;
+    } else if (T <= 4) {  // one block of fl_attn: splits of at least 128 positions, 64 per kv head at most
+        nch = span / 128;
         nch = nch > 64 ? 64 : nch;
     } else {
         nch = 512 / (nrb * KVH);
@@ -346,18 +646,26 @@ hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const 
     const dim3 grid(p.nrb * p.nch * KVH);
     const Launch L{st};
     hipError_t e;
-    if (fmt == 1)
-        e = T <= 4 ? launch(fl_attn<1, 1>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo, p.span,
-                            p.nch, p.nrb, ws)
-                   : launch(fl_attn<1, 2>, grid, dim3(512), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo, p.span,
-                            p.nch, p.nrb, ws);
+    if (T <= 2)  // decode (and 2-token steps): 16-row kernel
+        e = fmt == 1 ? launch(fl_dec16<1, FL_DEC_BUF>, dim3(p.nch * KVH), dim3(256), L, kp, vp, pe, rows, q, T, pos0,
+                              win, scale2, p.klo, p.span, p.nch, ws)
+                     : launch(fl_dec16<0, FL_DEC_BUF>, dim3(p.nch * KVH), dim3(256), L, kp, vp, pe, rows, q, T, pos0,
+                              win, scale2, p.klo, p.span, p.nch, ws);
+    else if (fmt == 1)  // blocks of 4 tokens: one wave group for 3-4 tokens, two for prefill
+        e = T <= 4 ? launch(fl_attn<1, 1, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
+                            p.span, p.nch, p.nrb, ws)
+                   : launch(fl_attn<1, 2, 2>, grid, dim3(512), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
+                            p.span, p.nch, p.nrb, ws);
     else
-        e = T <= 4 ? launch(fl_attn<0, 1>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo, p.span,
-                            p.nch, p.nrb, ws)
-                   : launch(fl_attn<0, 2>, grid, dim3(512), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo, p.span,
-                            p.nch, p.nrb, ws);
+        e = T <= 4 ? launch(fl_attn<0, 1, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
+                            p.span, p.nch, p.nrb, ws)
+                   : launch(fl_attn<0, 2, 2>, grid, dim3(512), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
+                            p.span, p.nch, p.nrb, ws);
     if (e != hipSuccess) return e;
-    return launch(fl_merge, dim3((T * QH + 7) / 8), dim3(256), L, (const float*)ws, T, p.nch, sinks, out);
+    if (p.nch > 8 * MERGE_J) return hipErrorInvalidValue;
+    if (p.nch <= MERGE_FEW)
+        return launch(fl_merge_few, dim3((T * QH + 7) / 8), dim3(256), L, (const float*)ws, T, p.nch, sinks, out);
+    return launch(fl_merge, dim3(T * QH), dim3(256), L, (const float*)ws, T, p.nch, sinks, out);
 }
 
 hipError_t launch_append(int fmt, void* kp, void* vp, int rows, int pos0, int ntok, const float* k, const float* v,
