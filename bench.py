@@ -324,6 +324,57 @@ def bench_cfg5(torch, mk, reps=3):
                 bit_identical=bool(same))
 
 
+def bench_flint(torch, mk, ctx=32768):
+    """The Flint KV path (no BASELINE config names it): one decode token and a 512-token prefill block on full layers
+    at `ctx` positions (8 layers rotated, so the K/V come from HBM) and on a sliding layer (1024-row ring, 513-position
+    window), f32 cache (the reference's default) and f16. µs per call of mfl_attend (attention + sink merge)."""
+    from mechta_amd import flint as mf
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2033)
+    res = {}
+
+    def timed(fn, it):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(it):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / it * 1000
+
+    L = 8
+    for fmt, name in ((mk.F32, "f32"), (mk.F16, "f16")):
+        st = mf.FlintStore(L + 1, ctx, fmt, sliding=[False] * L + [True])
+        k, v = seeded_normal(torch, gen, (512, 4, 128)), seeded_normal(torch, gen, (512, 4, 128))
+        for layer in range(L + 1):
+            for p0 in range(0, ctx, 512):
+                st.append(layer, p0, k, v)
+        q1, qb = seeded_normal(torch, gen, (1, 32, 128)), seeded_normal(torch, gen, (512, 32, 128))
+        sinks = seeded_normal(torch, gen, (32,))
+        o1, ob = torch.empty_like(q1), torch.empty_like(qb)
+        i = [0]
+
+        def dec():
+            st.attend(i[0] % L, ctx - 1, q1, sinks, o1)
+            i[0] += 1
+        us = timed(dec, 50)
+        bpe = 4 if fmt == mk.F32 else 2
+        res[f"{name}_decode_full_us"] = round(us, 2)
+        res[f"{name}_decode_full_gbps"] = round(ctx * 512 * bpe * 2 / (us * 1e-6) / 1e9, 1)
+        res[f"{name}_decode_sliding_us"] = round(timed(lambda: st.attend(L, ctx - 1, q1, sinks, o1), 50), 2)
+        us = timed(lambda: st.attend(0, ctx - 512, qb, sinks, ob), 5)
+        flops = 4 * 128 * 32 * sum(ctx - 512 + t + 1 for t in range(512))
+        res[f"{name}_prefill_full_us"] = round(us, 1)
+        res[f"{name}_prefill_full_tflops"] = round(flops / (us * 1e-6) / 1e12, 1)
+        res[f"{name}_prefill_sliding_us"] = round(timed(lambda: st.attend(L, ctx - 512, qb, sinks, ob), 5), 1)
+        st.close()
+    res["ctx"] = ctx
+    return res
+
+
 def cpu_baseline(dec, budget_s):
     """The oracle's attn_dmx + append on the bench's own cache, on this host's cores."""
     import numpy as np
@@ -407,6 +458,7 @@ def main():
         res["cfg4_us_per_position_10_layers"] = round(us4, 1)
         res["cfg4_kv_read_gbps"] = round(gbs4, 1)
         res["cfg5"] = bench_cfg5(torch, mk)
+        res["flint"] = bench_flint(torch, mk)
     if args.calib_copy:
         # plain elementwise copy of a known size: its FETCH_SIZE / WRITE_SIZE counters give the scale from counter
         # units to bytes for the KV kernels' counters in the same run

@@ -39,7 +39,7 @@ __device__ inline f32x16 mfma32f(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-// Window start of the token at position p: the 513 positions up to p on sliding layers (lo_di, flint_attn.wgsl:84).
+// Window start of the token at position p: the 513 positions up to p on sliding layers (lo_di, flint_attn.wgsl:82).
 __device__ inline int window_lo(int p, int win) { return win > 0 && p + 1 > win ? p + 1 - win : 0; }
 
 template <int FMT>
@@ -340,7 +340,7 @@ __global__ void __launch_bounds__(256) fl_append(void* __restrict__ kplane, void
     }
 }
 
-// NEOX RoPE: work-group (token, head), thread i rotates the pair (i, i + 64) (rope_neox_n, flint_attn.wgsl:49-57).
+// NEOX RoPE: work-group (token, head), thread i rotates the pair (i, i + 64) (rope_neox_n, flint_attn.wgsl:46-53).
 __global__ void __launch_bounds__(64) fl_rope(int heads, const float* __restrict__ x, const float* __restrict__ tab,
                                               float* __restrict__ out) {
 #pragma clang fp contract(off)
@@ -642,7 +642,7 @@ hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const 
                        const Plan& p, float* ws, const float* sinks, float* out, hipStream_t st) {
     if ((size_t)T * GQA * p.nch > 4096) return hipErrorInvalidValue;  // the workspace's rows x splits per kv head
     const size_t pe = (size_t)rows * HD;
-    const float scale2 = (1.0f / 11.313708498984761f) * LOG2E;  // 1/sqrt(128) (flint_attn.wgsl:86) in log2 units
+    const float scale2 = (1.0f / 11.313708498984761f) * LOG2E;  // 1/sqrt(128) (flint_attn.wgsl:92, 189) in log2 units
     const dim3 grid(p.nrb * p.nch * KVH);
     const Launch L{st};
     hipError_t e;

@@ -1,8 +1,8 @@
 // flint_store.cpp -- the Flint KV store and its C ABI (include/mechta_flint.h).
 //
 // Replaces the K/V buffers of Flint::new (flint.rs:227-232), the per-token uniforms (n, slot, lo, ring) that
-// Flint::inputs writes for every layer (flint.rs:296-300) and the prefill block's (flint.rs:363-368), the root copies
-// (read_root / write_root, flint.rs:324-336) and the ring photo (flint.rs:311-320).
+// Flint::inputs writes for every layer (flint.rs:294-298) and the prefill block's (flint.rs:358-362), the root copies
+// (read_root / write_root, flint.rs:320-331) and the ring photo (flint.rs:308-316).
 #include <hip/hip_runtime.h>
 
 #include <cmath>

@@ -51,7 +51,7 @@ def _check(rc):
 
 
 def rope_table(pos, base=10000.0):
-    """rope_table(pos, base) of flint.rs:71-78, computed by the library's host code: 128 floats."""
+    """rope_table(pos, base) of flint.rs:61-68, computed by the library's host code: 128 floats."""
     buf = (ctypes.c_float * HEAD_DIM)()
     _check(lib().mfl_rope_table(int(pos), float(base), buf))
     return list(buf)

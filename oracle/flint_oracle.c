@@ -5,7 +5,7 @@
  * or calls this file. Built into libmkv_oracle.so by oracle/build.py (gcc -O3 -fopenmp -ffp-contract=off).
  *
  * Caches here use the reference's layout: per layer a K and a V array of `ring` rows x 512 elements (row = position %
- * ring, 4 KV heads x 128), f32 values or f16 bit patterns (kv_put of the f16 block, flint.rs:91-98: pack2x16float).
+ * ring, 4 KV heads x 128), f32 values or f16 bit patterns (kv_put of the f16 block, flint.rs:83-90: pack2x16float).
  *
  * Parity pinning (tests/test_oracle.py): the RoPE table against float64 cos/sin of the f32 angle recurrence; RoPE
  * against float64 rotation and the identity at position 0; the writes against numpy's float16 cast and the ring
@@ -25,9 +25,9 @@
 #define FL_KVH 4
 #define FL_D 128
 #define FL_ROW (FL_KVH * FL_D)
-#define NEG_BIG (-3.0e38f) /* flint_attn.wgsl:113, 205 */
+#define NEG_BIG (-3.0e38f) /* flint_attn.wgsl:128, 202 */
 
-/* rope_table (flint.rs:71-78): scale = base^(-2/128) in f32, theta_0 = pos, theta_{i+1} = theta_i * scale. */
+/* rope_table (flint.rs:61-68): scale = base^(-2/128) in f32, theta_0 = pos, theta_{i+1} = theta_i * scale. */
 void orc_fl_rope_table(int pos, float base, float* tab) {
     float scale = powf(base, -2.0f / (float)FL_D);
     float theta = (float)pos;
@@ -38,7 +38,7 @@ void orc_fl_rope_table(int pos, float base, float* tab) {
     }
 }
 
-/* rope_neox_n (flint_attn.wgsl:49-57): pair (i, i + 64) of each 128-row; rows = ntok * heads, row r uses table row
+/* rope_neox_n (flint_attn.wgsl:46-53): pair (i, i + 64) of each 128-row; rows = ntok * heads, row r uses table row
  * r / heads. */
 void orc_fl_rope(int ntok, int heads, const float* x, const float* tab, float* out) {
     for (int r = 0; r < ntok * heads; r++) {
@@ -60,7 +60,7 @@ static float kv_elem(int fmt, const void* c, size_t i) {
     return orc_f16_to_f32(((const uint16_t*)c)[i]);
 }
 
-/* kv_write_n (flint_attn.wgsl:59-65): token t of the block into row (pos0 + t) % ring. */
+/* kv_write_n (flint_attn.wgsl:56-61): token t of the block into row (pos0 + t) % ring. */
 void orc_fl_kv_write(int fmt, void* kc, void* vc, int ring, int pos0, int n, const float* k, const float* v) {
     for (int t = 0; t < n; t++) {
         size_t r = (size_t)((pos0 + t) % ring) * FL_ROW;
@@ -84,7 +84,7 @@ static float dot4(const float* a, const float* b) {
 
 #define FD_CH 256
 
-/* attn_fd + attn_fd_merge (flint_attn.wgsl:188-257) of one token: q [32][128]; positions lo .. lo + n - 1 at rows
+/* attn_fd + attn_fd_merge (flint_attn.wgsl:172-257) of one token: q [32][128]; positions lo .. lo + n - 1 at rows
  * pos % ring; pieces of 256 positions: per (head, piece) max, sum of exp and exp-weighted V; then the merge with the
  * sink. out [32][128]. sinks may be NULL (no sink term). */
 void orc_fl_attn_fd(int fmt, const void* kc, const void* vc, int ring, const float* q, int lo, int n,
@@ -153,7 +153,7 @@ void orc_fl_attn_fd(int fmt, const void* kc, const void* vc, int ring, const flo
 
 static int lo_di(int pos, int win) { return win > 0 && pos + 1 > win ? pos + 1 - win : 0; }
 
-/* attn_pf (flint_attn.wgsl:67-183, with Q, K, V kept in f32 as attn_source makes it): per (KV head, group of 8
+/* attn_pf (flint_attn.wgsl:63-170, with Q, K, V kept in f32 as attn_source makes it): per (KV head, group of 8
  * tokens), 64-key tiles from the group's first token's window start; exact online softmax per row with the running
  * maximum starting at the sink and the running sum at 1 (its exp); token T sees [lo_T, pos0 + T]. q, out:
  * [n][32][128]. sinks may be NULL (running max -3e38, sum 0). */
