@@ -15,8 +15,8 @@ LIB = os.path.join(OUTDIR, "libmechta_kv.so")
 SOURCES = ["kv_store.cpp", "kv_root.cpp", "kv_append.hip", "kv_produce.hip", "kv_decode.hip", "kv_prefill.hip",
            "kv_attn32.hip", "flint_store.cpp", "flint_kv.hip"]
 # prefill: MFMA accumulators in VGPRs, so the rare lazy rescale of O is plain VALU work instead of AGPR round trips
-# kv_decode, kv_attn32: no NaN handling in fmaxf (masked scores are -inf, never NaN), so max reductions need no canonicalize
-EXTRA = {"kv_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"], "kv_decode.hip": ["-fno-honor-nans"],
+# kv_prefill, kv_decode, kv_attn32: no NaN handling in fmaxf (masked scores are -inf, never NaN), so max reductions need no canonicalize
+EXTRA = {"kv_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"], "kv_decode.hip": ["-fno-honor-nans"],
          "kv_attn32.hip": ["-fno-honor-nans"], "flint_kv.hip": ["-fno-honor-nans"],
          "kv_produce.hip": ["-ffp-contract=off"]}
 ARCH = os.environ.get("MKV_OFFLOAD_ARCH", "gfx950")

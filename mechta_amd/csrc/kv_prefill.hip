@@ -150,12 +150,25 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
         f32x16 Scur[RB];
 #pragma unroll
         for (int b = 0; b < RB; b++) Scur[b] = f32x16{};
+        constexpr int KP = 3;  // K operands in flight ahead of the S chain (LDS latency; registers allow 3)
+        half8 kbuf[KP];
+#pragma unroll
+        for (int s = 0; s < KP; s++) kbuf[s] = *(const half8*)(Ks + kaddr + s * 1024);
 #pragma unroll
         for (int s = 0; s < 16; s++) {
-            const half8 ka = *(const half8*)(Ks + kaddr + s * 1024);
+            const half8 ka = kbuf[s % KP];
+            if (s + KP < 16) kbuf[s % KP] = *(const half8*)(Ks + kaddr + (s + KP) * 1024);
 #pragma unroll
             for (int b = 0; b < RB; b++) Scur[b] = mfma32(ka, qb[b][s], Scur[b]);
         }
+        // schedule: KP LDS reads (mask 0x100), then alternately one MFMA (0x008) and the next LDS read
+        __builtin_amdgcn_sched_group_barrier(0x100, KP, 0);
+#pragma unroll
+        for (int s = 0; s < 16 - KP; s++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, KP, 0);
         half8 pa[RB][2];
 #pragma unroll
         for (int b = 0; b < RB; b++) {
@@ -173,7 +186,7 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             float mt = Scur[b][0];
 #pragma unroll
             for (int i = 1; i < 16; i++) mt = fmaxf(mt, Scur[b][i]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            mt = xor32_op(mt, [](float a, float b) { return fmaxf(a, b); });
             float mr = m[b];
             if (m[b] == NEG_INF || mt > m[b] + LAZY2) mr = fmaxf(m[b], mt);
             const float cf = (m[b] == NEG_INF) ? 1.f : fast_exp2(m[b] - mr);
@@ -198,14 +211,25 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             }
             lsum[b] = lsum[b] * cf + ls;
         }
+        constexpr int VP = 3;  // V operands in flight ahead of the P.V MFMAs
+        half8 vbuf[VP];
+        auto vaddr = [&](int i) { return Vs + (2 * (i >> 3) + h) * 4096 + (32 * (i & 7) + r) * 16; };
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++)
+        for (int i = 0; i < VP; i++) vbuf[i] = *(const half8*)vaddr(i);
 #pragma unroll
-            for (int nb = 0; nb < 8; nb++) {
-                const half8 vb = *(const half8*)(Vs + (2 * s2 + h) * 4096 + (32 * nb + r) * 16);
+        for (int i = 0; i < 16; i++) {
+            const half8 vb = vbuf[i % VP];
+            if (i + VP < 16) vbuf[i % VP] = *(const half8*)vaddr(i + VP);
 #pragma unroll
-                for (int b = 0; b < RB; b++) O[b][nb] = mfma32(pa[b][s2], vb, O[b][nb]);
-            }
+            for (int b = 0; b < RB; b++) O[b][i & 7] = mfma32(pa[b][i >> 3], vb, O[b][i & 7]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, VP, 0);
+#pragma unroll
+        for (int i = 0; i < 16 - VP; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, VP, 0);
       }
     }
 
