@@ -172,21 +172,20 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
         half8 pa[RB][2];
 #pragma unroll
         for (int b = 0; b < RB; b++) {
-            // scale (log2 units); the causal / start mask only where this tile crosses a row's window
-            if (__all(k0 >= start && k0 + 32 <= vis[b])) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) Scur[b][i] *= scale2;
-            } else {
+            // the causal / start mask only where this tile crosses a row's window (raw scores; the scale, log2
+            // units, is applied to the max and inside the exponent's FMA)
+            if (!__all(k0 >= start && k0 + 32 <= vis[b])) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int key = k0 + 8 * h + i + (i >= 8 ? 8 : 0);
-                    Scur[b][i] = (key < vis[b] && key >= start) ? Scur[b][i] * scale2 : NEG_INF;
+                    Scur[b][i] = (key < vis[b] && key >= start) ? Scur[b][i] : NEG_INF;
                 }
             }
             float mt = Scur[b][0];
 #pragma unroll
             for (int i = 1; i < 16; i++) mt = fmaxf(mt, Scur[b][i]);
             mt = xor32_op(mt, [](float a, float b) { return fmaxf(a, b); });
+            mt *= scale2;  // scale2 > 0: the max of the scaled scores is the scaled max
             float mr = m[b];
             if (m[b] == NEG_INF || mt > m[b] + LAZY2) mr = fmaxf(m[b], mt);
             const float cf = (m[b] == NEG_INF) ? 1.f : fast_exp2(m[b] - mr);
@@ -199,13 +198,13 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
                 }
             }
             m[b] = mr;
-            // P = 2^(s - m): masked scores are -inf and give 0 (the reference is 0 while a row has seen no key);
+            // P = 2^(s * scale2 - m) (one FMA): masked scores are -inf and give 0 (the reference is 0 while a row has seen no key);
             // the row sum takes the f32 P, as attn_fa_mx does, the P.V operand its f16 rounding
             const float base = mr == NEG_INF ? 0.f : mr;
             float ls = 0.f;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float p = fast_exp2(Scur[b][i] - base);
+                const float p = fast_exp2(__builtin_fmaf(Scur[b][i], scale2, -base));
                 ls += p;
                 pa[b][i >> 3][i & 7] = (_Float16)p;
             }
