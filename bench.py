@@ -375,6 +375,27 @@ def bench_flint(torch, mk, ctx=32768):
     return res
 
 
+def bench_read_floor(torch, nbytes, nbuf=10, reps=60):
+    """A plain streaming read of nbytes by one launch (libmkv_probe.so: 248 work-groups, 64 KB stages dealt round
+    robin, non-temporal 16-byte loads, two stages in flight), over nbuf different buffers in turn so that nothing
+    comes from the 256 MB last-level cache; durations from the dispatch timestamps, as for the decode kernel."""
+    import ctypes
+    here = os.path.dirname(os.path.abspath(__file__))
+    probe = ctypes.CDLL(os.path.join(here, "mechta_amd", "lib", "libmkv_probe.so"))
+    nbytes = (nbytes + 65535) // 65536 * 65536
+    bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(nbuf)]
+    torch.cuda.synchronize()
+    ptrs = (ctypes.c_void_p * nbuf)(*[b.data_ptr() for b in bufs])
+    mean, best = ctypes.c_float(), ctypes.c_float()
+    rc = probe.mkv_probe_read(ptrs, nbuf, ctypes.c_size_t(nbytes), 248, reps, ctypes.byref(mean), ctypes.byref(best))
+    if rc != 0:
+        raise RuntimeError(f"mkv_probe_read failed: HIP error {rc}")
+    del bufs
+    return {"bytes": nbytes, "mean_us": round(mean.value, 2), "best_us": round(best.value, 2),
+            "gbps": round(nbytes / (mean.value * 1e-6) / 1e9, 1),
+            "what": "one launch of a plain streaming read of the decode launch's K+V bytes (libmkv_probe.so)"}
+
+
 def cpu_baseline(dec, budget_s):
     """The oracle's attn_dmx + append on the bench's own cache, on this host's cores."""
     import numpy as np
@@ -459,6 +480,7 @@ def main():
         res["cfg4_kv_read_gbps"] = round(gbs4, 1)
         res["cfg5"] = bench_cfg5(torch, mk)
         res["flint"] = bench_flint(torch, mk)
+        res["hbm_read_floor"] = bench_read_floor(torch, int(core_bytes))
     if args.calib_copy:
         # plain elementwise copy of a known size: its FETCH_SIZE / WRITE_SIZE counters give the scale from counter
         # units to bytes for the KV kernels' counters in the same run

@@ -1,4 +1,5 @@
-"""Builds libmechta_kv.so (the HIP path and its C ABI) in-tree for gfx950 with hipcc.
+"""Builds libmechta_kv.so (the HIP path and its C ABI) in-tree for gfx950 with hipcc, and libmkv_probe.so (bench.py's
+plain-read probe, no part of the ABI).
 
 Every HIP source is compiled with -Xclang -target-feature -Xclang -packed-fp32-ops (no packed-FP32 instructions) and
 linked into mechta_amd/lib/libmechta_kv.so. The library has no dependency on torch or on oracle/.
@@ -19,6 +20,8 @@ SOURCES = ["kv_store.cpp", "kv_root.cpp", "kv_append.hip", "kv_produce.hip", "kv
 EXTRA = {"kv_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"], "kv_decode.hip": ["-fno-honor-nans"],
          "kv_attn32.hip": ["-fno-honor-nans"], "flint_kv.hip": ["-fno-honor-nans"],
          "kv_produce.hip": ["-ffp-contract=off"]}
+# measurement aid of bench.py (a plain HBM read of a given size), its own library: not part of the KV-cache ABI
+PROBE_SRC, PROBE_LIB = "hbm_probe.hip", os.path.join(OUTDIR, "libmkv_probe.so")
 ARCH = os.environ.get("MKV_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -44,14 +47,15 @@ def _compile(src, verbose):
 
 def build(verbose=False):
     os.makedirs(OUTDIR, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB)
+    with ThreadPoolExecutor(max_workers=len(SOURCES) + 1) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES + [PROBE_SRC]))
+    for lib, o in ((LIB, objs[:-1]), (PROBE_LIB, objs[-1:])):
+        tmp = lib + ".tmp"
+        cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + o
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        os.replace(tmp, lib)
     return LIB
 
 
