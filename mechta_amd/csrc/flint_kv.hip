@@ -96,11 +96,11 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
 #pragma unroll
             for (int m = 0; m < 4; m++)
                 X.k[m] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       kr, b + ((8 * w + 2 * m + s) * TILE + r32) * 16, 0, 0));
+                                                       kr, b + ((8 * w + 2 * m + s) * TILE + r32) * 16, 0, LOAD_NT));
 #pragma unroll
             for (int qq = 0; qq < 4; qq++)
                 X.v[qq] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        vr, b + ((2 * qq + s) * HD + 32 * w + r32) * 16, 0, 0));
+                                                        vr, b + ((2 * qq + s) * HD + 32 * w + r32) * 16, 0, LOAD_NT));
         } else {
 #pragma unroll
             for (int a = 0; a < 2; a++)
@@ -108,7 +108,7 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
 #pragma unroll
             for (int qq = 0; qq < 4; qq++)
                 X.v[qq] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(
-                                                        vr, b + (qq * HD + 32 * w + r32) * 16 + 8 * s, 0, 0));
+                                                        vr, b + (qq * HD + 32 * w + r32) * 16 + 8 * s, 0, LOAD_NT));
         }
     };
 
@@ -430,11 +430,11 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
 #pragma unroll
             for (int a = 0; a < 8; a++)
                 X.k[a] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       kr, blk + ((4 * a + g) * 32 + sub + r16) * 16, 0, 0));
+                                                       kr, blk + ((4 * a + g) * 32 + sub + r16) * 16, 0, LOAD_NT));
 #pragma unroll
             for (int cc = 0; cc < 8; cc++)
                 X.v[cc] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        vr, blk + ((sub / 4 + g) * HD + 16 * cc + r16) * 16, 0, 0));
+                                                        vr, blk + ((sub / 4 + g) * HD + 16 * cc + r16) * 16, 0, LOAD_NT));
         } else {
 #pragma unroll
             for (int a = 0; a < 4; a++) X.k[a] = bload16(kr, blk + ((4 * a + g) * 32 + sub + r16) * 16);
