@@ -5,16 +5,25 @@
 // Work-group (block of 4 tokens, key split, kv head): 32 query rows (token * 8 + head) against the split's keys in
 // tiles of 32 keys, by NWG groups of 4 waves that take alternate tiles. Prefill runs two groups (two waves per SIMD:
 // one group's MFMAs run while the other waits for its loads; their states are merged through LDS at the end). Decode
-// runs one: its splits are only 4-5 tiles long, too few to share. Per tile, wave w of a group
-//   S^T[32 keys][32 rows] over dims 64w .. 64w+63    32 x v_mfma_f32_32x32x2_f32, A = K straight from HBM, B = Q (LDS)
+// runs one: its splits are only 4-5 tiles long, too few to share.
+//
+// f32 products on the f16 matrix units: each f32 operand x is split into hi = f16(x) and lo = f16(x - hi), and a
+// product a.b is taken as hi(a)hi(b) + hi(a)lo(b) + lo(a)hi(b) (three v_mfma_f32_32x32x16_f16, f32 accumulation; the
+// dropped lo.lo term is below 2^-22 of |a||b|). The f16 matrix units run 32x32x16 in the time the f32 ones take for
+// 32x32x2, so the three passes cost 3/8 of one f32 pass, and the path keeps f32-level accuracy (within 1e-5 of the
+// exact-f32 reference). Per tile, wave w of a group computes
+//   S^T[32 keys][32 rows] over dims 64w .. 64w+63    4 dim steps x 3 passes; A = K split from its HBM loads, B = Q
+//                                                     (split once into LDS)
 //   the four partial S^T summed through LDS ((w0 + w1) + (w2 + w3), the same order in every wave)
 //   exact-max online softmax of the 32 rows (each wave redundantly: 16 scores per lane)
-//   O[32 rows][dims 64w .. 64w+63] += P . V           32 x v_mfma_f32_32x32x2_f32, A = P (the S^T registers), B = V
-// The 32x32 accumulator layout gives lane l (half s = l / 32) row l % 32 and keys 8a + 4s + b (register 4a + b).
-// Those are the keys the A operand of the P.V MFMAs needs in that lane, so P never leaves the registers, and they are
-// four consecutive keys per register quad: with V stored [pos/4][d][pos%4] each quad's operand is one 16-byte load.
-// K is stored [pos/32][d/4][pos%32][4], so a lane's 16-byte K load is 4 dims of key l % 32 and a wave's load is two
-// 512-byte runs. Tiles are double-buffered in registers: the loads of tile j + 1 fly while tile j computes.
+//   O[32 rows][dims 64w .. 64w+63] += P . V           2 key steps x 2 dim blocks x 3 passes; A = P split from the
+//                                                     S^T registers, B = V split from its HBM loads
+// The 32x32 accumulator layout gives lane l (half s = l / 32) row l % 32 and keys 8a + 4s + b (register 4a + b). A
+// 16-key step k of P.V takes, in lane half s, the keys 16k + 4s + b and 16k + 8 + 4s + b (b < 4): the step's keys
+// are summed in any order as long as P and V agree on it, so P never leaves the registers, and with V stored
+// [pos/4][d][pos%4] each four keys of a dim are one 16-byte load. K is stored [pos/32][d/4][pos%32][4]: a lane's
+// 16-byte K load is 4 dims of key l % 32. Tiles are double-buffered in registers: the loads of tile j + 1 fly while
+// tile j computes.
 #include "mkv_device.h"
 
 namespace mkv {
@@ -22,21 +31,34 @@ namespace {
 
 constexpr int TILE = 32;                       // keys per tile: one K block, eight V groups
 constexpr unsigned TILE_BYTES = TILE * HD * 4;  // 32 KB of each plane
-constexpr int QPAD = HD + 4;                   // LDS row of Q (floats): rows 4 banks apart
+constexpr int QPAD = HD + 8;                   // LDS row of Q's halves: 16-byte reads of 32 rows conflict-free
 
-__device__ inline f32x16 mfma32f(float a, float b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+// x = hi + lo to 2^-22: hi = f16(x), lo = f16(x - hi) (the residual is exact in f32)
+__device__ inline void split8(f32x4 a, f32x4 b, half8& hi, half8& lo) {
+    hi = half8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+               (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+    lo = half8{(_Float16)(a.x - (float)hi[0]), (_Float16)(a.y - (float)hi[1]), (_Float16)(a.z - (float)hi[2]),
+               (_Float16)(a.w - (float)hi[3]), (_Float16)(b.x - (float)hi[4]), (_Float16)(b.y - (float)hi[5]),
+               (_Float16)(b.z - (float)hi[6]), (_Float16)(b.w - (float)hi[7])};
+}
+// c += a.b with a = ah + al, b = bh + bl: three f16 MFMAs (al.bl dropped)
+__device__ inline f32x16 mfma3(half8 ah, half8 al, half8 bh, half8 bl, f32x16 c) {
+    c = mfma32(ah, bh, c);
+    c = mfma32(ah, bl, c);
+    return mfma32(al, bh, c);
 }
 __device__ inline f32x4 bload4f(rsrc_t r, unsigned off) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, LOAD_NT));
 }
 
 struct Tile {
-    f32x4 k[8];  // K: dims 64w + 8m + 4s .. +3 of key l % 32 (m = 0..7)
-    f32x4 v[8];  // V: keys 8q + 4s .. +3 of dim 64w + 32c + l % 32 (index 4c + q)
+    f32x4 k[8];  // K: dims 64w + 16k + 8s + 4e .. +3 of key l % 32 (index 2k + e)
+    f32x4 v[8];  // V: keys 16k + 8e + 4s .. +3 of dim 64w + 32c + l % 32 (index 4k + 2c + e)
 };
 
-template <int NWG>  // wave groups
+// NWG wave groups; NBUF tiles in registers, NBUF - 1 of them loading while one computes (2: deeper prefetch measured
+// slower from HBM, 3 tiles 2 us and 4 tiles 5 us more per 16K-position decode)
+template <int NWG, int NBUF>
 __global__ void __launch_bounds__(256 * NWG) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
                                                 size_t plane_elems, const float* __restrict__ q, int T, int n,
                                                 int start, float scale2, int span, int nch, int c0, int nrb, int rpk,
@@ -50,47 +72,71 @@ __global__ void __launch_bounds__(256 * NWG) attn_f32(const float* __restrict__ 
     const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 8, w = (tid >> 6) & 3, s = lane >> 5, r32 = lane & 31;
     const int t0 = 4 * rb, nt = min(4, T - t0);
     const int kend = n + T - 1;  // keys of the whole call
-    const int cs = chunk_lo(c, span, nch), ce = c + 1 < nch ? chunk_lo(c + 1, span, nch) : kend;
-    const int lo = max(cs, start / TILE * TILE), hi = min(ce, n + t0 + nt - 1);  // hi: the block's last key + 1
-    const int ntile = hi > lo ? (hi - lo + TILE - 1) / TILE : 0;
+    // span > 0: work-group c takes the contiguous split [chunk_lo(c), chunk_lo(c + 1)) (prefill: the token blocks of
+    // a split share its keys through one L2). span == 0 (decode): the 32-key tiles from the window start on are dealt
+    // round robin, tile c + j * nch to work-group c, so at any moment the work-groups stream neighbouring tiles.
+    int lo, hi, ntile, tstep;  // tile j of this work-group starts at key lo + j * tstep * TILE; keys < hi are its
+    if (span > 0) {
+        const int cs = chunk_lo(c, span, nch), ce = c + 1 < nch ? chunk_lo(c + 1, span, nch) : kend;
+        lo = max(cs, start / TILE * TILE);
+        hi = min(ce, n + t0 + nt - 1);  // the block's last key + 1
+        ntile = hi > lo ? (hi - lo + TILE - 1) / TILE : 0;
+        tstep = 1;
+    } else {
+        const int lo0 = start / TILE * TILE;
+        hi = n + t0 + nt - 1;
+        const int nt_all = (hi - lo0 + TILE - 1) / TILE;
+        lo = lo0 + c * TILE;
+        ntile = c < nt_all ? (nt_all - c + nch - 1) / nch : 0;
+        tstep = nch;
+    }
 
-    __shared__ float qs[ROWS][QPAD];
+    __shared__ __attribute__((aligned(16))) _Float16 qh[ROWS][QPAD], ql[ROWS][QPAD];  // Q split: hi, lo
     __shared__ f32x4 sx[2][NWG][4][4][64];  // partial S^T: [tile parity][group][wave][register quad][lane]
-    for (int i = tid; i < ROWS * HD / 4; i += 256 * NWG) {
-        const int row = i / (HD / 4), d4 = (i % (HD / 4)) * 4, t = t0 + (row >> 3);
-        f32x4 x = f32x4{};
-        if (t < T) x = *(const f32x4*)(q + ((size_t)t * QH + kvh * GQA + (row & 7)) * HD + d4);
-        *(f32x4*)&qs[row][d4] = x;
+    for (int i = tid; i < ROWS * HD / 8; i += 256 * NWG) {
+        const int row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
+        f32x4 x0 = f32x4{}, x1 = f32x4{};
+        if (t < T) {
+            const float* qr = q + ((size_t)t * QH + kvh * GQA + (row & 7)) * HD + d8;
+            x0 = *(const f32x4*)qr;
+            x1 = *(const f32x4*)(qr + 4);
+        }
+        half8 hi, lo;
+        split8(x0, x1, hi, lo);
+        *(half8*)&qh[row][d8] = hi;
+        *(half8*)&ql[row][d8] = lo;
     }
     __syncthreads();
 
     // tile j of this split starts at key lo + 32j, at the same byte offset j * 32 KB in both planes; loads of tile
     // ntile (the prefetch after the last) lie past the resources and return zeros without a memory access
-    const unsigned rbytes = (unsigned)ntile * TILE_BYTES;
+    const unsigned rbytes = ntile > 0 ? (unsigned)((ntile - 1) * tstep + 1) * TILE_BYTES : 0u;
     const rsrc_t kr = plane_rsrc(kplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
     const rsrc_t vr = plane_rsrc(vplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
-    const unsigned kofs = ((16 * w + s) * (TILE * 4) + r32 * 4) * 4;  // + m * 2 * 512 B
-    const unsigned vofs = (s * (4 * HD) + (64 * w + r32) * 4) * 4;    // + q * 2 * 4 KB + c * 32 dims * 16 B
+    const unsigned kofs = ((16 * w + 2 * s) * TILE + r32) * 16;  // + (4k + e) * 512 B: dims 64w + 16k + 8s + 4e
+    const unsigned vofs = (s * HD + 64 * w + r32) * 16;            // + (4k + 2e) * 4 KB + c * 32 dims * 16 B
     auto load = [&](Tile& X, int j) {
-        const unsigned base = (unsigned)j * TILE_BYTES;
+        const unsigned base = (unsigned)(j * tstep) * TILE_BYTES;
 #pragma unroll
-        for (int m = 0; m < 8; m++) X.k[m] = bload4f(kr, base + kofs + m * (2 * TILE * 4 * 4));
+        for (int i = 0; i < 8; i++) X.k[i] = bload4f(kr, base + kofs + ((i >> 1) * 4 + (i & 1)) * (TILE * 16));
 #pragma unroll
-        for (int cq = 0; cq < 8; cq++)
-            X.v[cq] = bload4f(vr, base + vofs + (cq & 3) * (2 * 4 * HD * 4) + (cq >> 2) * (32 * 4 * 4));
+        for (int i = 0; i < 8; i++)
+            X.v[i] = bload4f(vr, base + vofs + ((i >> 2) * 4 + 2 * (i & 1)) * (HD * 16) + ((i >> 1) & 1) * (32 * 16));
     };
 
     const int vis = n + t0 + (r32 >> 3);  // lane's row sees keys < vis (and of this split, < hi)
     float m_run = NEG_INF, l_run = 0.f;
     f32x16 O[2] = {f32x16{}, f32x16{}};
     auto step = [&](Tile& X, int j) {
-        const int k0 = lo + j * TILE;
+        const int k0 = lo + j * tstep * TILE;
         f32x16 S = f32x16{};
 #pragma unroll
-        for (int m = 0; m < 8; m++) {
-            const f32x4 qv = *(const f32x4*)&qs[r32][64 * w + 8 * m + 4 * s];
-#pragma unroll
-            for (int b = 0; b < 4; b++) S = mfma32f(X.k[m][b], qv[b], S);
+        for (int k = 0; k < 4; k++) {
+            half8 kh, kl;
+            split8(X.k[2 * k], X.k[2 * k + 1], kh, kl);
+            const half8 bh = *(const half8*)&qh[r32][64 * w + 16 * k + 8 * s];
+            const half8 bl = *(const half8*)&ql[r32][64 * w + 16 * k + 8 * s];
+            S = mfma3(kh, kl, bh, bl, S);
         }
         const int pb = (j / NWG) & 1;
         f32x4(&sg)[4][4][64] = sx[pb][grp];
@@ -138,30 +184,38 @@ __global__ void __launch_bounds__(256 * NWG) attn_f32(const float* __restrict__ 
         // keys past the block's last (unwritten or stale rows) have P = 0 and must not bring NaN in through V
         if (k0 + TILE > hi) {
 #pragma unroll
-            for (int cq = 0; cq < 8; cq++)
+            for (int i = 0; i < 8; i++)
 #pragma unroll
                 for (int b = 0; b < 4; b++)
-                    if (k0 + 8 * (cq & 3) + 4 * s + b >= hi) X.v[cq][b] = 0.f;
+                    if (k0 + 16 * (i >> 2) + 8 * (i & 1) + 4 * s + b >= hi) X.v[i][b] = 0.f;
         }
 #pragma unroll
-        for (int cc = 0; cc < 2; cc++)
+        for (int k = 0; k < 2; k++) {
+            half8 ph, pl;  // P of keys 16k + 4s + b and 16k + 8 + 4s + b: registers 8k + b and 8k + 4 + b
+            split8(f32x4{sv[8 * k], sv[8 * k + 1], sv[8 * k + 2], sv[8 * k + 3]},
+                   f32x4{sv[8 * k + 4], sv[8 * k + 5], sv[8 * k + 6], sv[8 * k + 7]}, ph, pl);
 #pragma unroll
-            for (int qq = 0; qq < 4; qq++)
-#pragma unroll
-                for (int b = 0; b < 4; b++) O[cc] = mfma32f(sv[4 * qq + b], X.v[4 * cc + qq][b], O[cc]);
+            for (int cc = 0; cc < 2; cc++) {
+                half8 vh, vl;
+                split8(X.v[4 * k + 2 * cc], X.v[4 * k + 2 * cc + 1], vh, vl);
+                O[cc] = mfma3(ph, pl, vh, vl, O[cc]);
+            }
+        }
     };
 
     // group g takes tiles g, g + 2, ...; both run the same number of rounds (every wave meets every barrier): a round
     // past the last tile loads nothing (zeros) and has every key masked
     const int rounds = (ntile + NWG - 1) / NWG;
-    Tile A, B;
-    load(A, grp);
-    for (int i = 0; i < rounds; i += 2) {
-        load(B, (i + 1) * NWG + grp);
-        step(A, i * NWG + grp);
-        if (i + 1 >= rounds) break;
-        load(A, (i + 2) * NWG + grp);
-        step(B, (i + 1) * NWG + grp);
+    Tile X[NBUF];
+#pragma unroll
+    for (int b = 0; b < NBUF - 1; b++) load(X[b], b * NWG + grp);
+    for (int i = 0; i < rounds; i += NBUF) {
+#pragma unroll
+        for (int b = 0; b < NBUF; b++) {
+            if (i + b >= rounds) break;
+            load(X[(b + NBUF - 1) % NBUF], (i + b + NBUF - 1) * NWG + grp);
+            step(X[b], (i + b) * NWG + grp);
+        }
     }
 
     // merge group 1 into group 0 through LDS (the parity buffers are free after the barrier)
@@ -221,17 +275,18 @@ __global__ void __launch_bounds__(256 * NWG) attn_f32(const float* __restrict__ 
 Attn32Plan attn32_plan(int T, int n, int start) {
     const int kend = n + T - 1;
     const int nrb = (T + 3) / 4;
-    int nch;
     if (T <= 4) {
-        // decode: splits of at least 128 positions, at most 124 per kv head (248 work-groups on the 256 CUs)
-        nch = kend / 128;
-        nch = nch > 124 ? 124 : nch;
-    } else {
-        // prefill: about two work-groups per CU, splits of at least 128 positions, at most 16 (one merge round trip)
-        nch = 512 / (nrb * KVH);
-        const int most = kend / 128;
-        nch = nch > most ? most : nch > 16 ? 16 : nch;
+        // decode: the window's tiles dealt round robin to at most 124 work-groups per kv head (248 on the 256 CUs),
+        // at least 4 tiles each; every work-group holds keys of every row, so the merge reads all (span 0)
+        int nch = (kend - start / TILE * TILE) / 128;
+        nch = nch > 124 ? 124 : nch < 1 ? 1 : nch;
+        return Attn32Plan{0, nch, 0, nrb};
     }
+    // prefill: contiguous splits, about two work-groups per CU, splits of at least 128 positions, at most 16 (one
+    // merge round trip)
+    int nch = 512 / (nrb * KVH);
+    const int most = kend / 128;
+    nch = nch > most ? most : nch > 16 ? 16 : nch;
     nch = nch < 1 ? 1 : nch;
     int c0, c1;  // splits wholly below `start` get no work-group
     chunk_range(start, kend, kend, nch, c0, c1);
@@ -246,9 +301,9 @@ hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const flo
     const float* vp = (const float*)(b + g.plane(layer, 1, 0) * g.plane_bytes());
     dim3 grid(p.nrb * (p.nch - p.c0) * KVH);
     if (T <= 4)
-        return launch(attn_f32<1>, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
+        return launch(attn_f32<1, 2>, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
                       p.nch, p.c0, p.nrb, rpk, part);
-    return launch(attn_f32<2>, grid, dim3(512), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
+    return launch(attn_f32<2, 2>, grid, dim3(512), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
                   p.nch, p.c0, p.nrb, rpk, part);
 }
 

@@ -158,7 +158,8 @@ hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, 
 hipError_t launch_qk_produce(int ntok, const float* qf, const float* kb, const float* q_w, const float* k_w,
                              float eps, const float* tab, float* q_out, float* kn_out, const Launch& L);
 // Attention over the f32 store (kv_attn32.hip), decode (T <= 4) and prefill alike: nrb blocks of 4 tokens, splits
-// [c0, nch) of [0, span) (chunk_lo); partials [kvh][row < rpk][nch][PART], then launch_merge.
+// [c0, nch) of [0, span) (chunk_lo), or for decode (span 0) nch work-groups per kv head taking the window's 32-key
+// tiles round robin; partials [kvh][row < rpk][nch][PART], then launch_merge.
 struct Attn32Plan {
     int span, nch, c0, nrb;
 };
