@@ -2,14 +2,17 @@
 // sliding-window attention with per-head sinks (flint_attn.wgsl:1-257), for one decode token or a prefill block.
 //
 // Attention work-group: (block of 4 tokens, key split, kv head) = 32 query rows (token * 8 + head) against the split's
-// keys in tiles of 32 positions, on the fp32 matrix cores (v_mfma_f32_32x32x2_f32; f16 caches are widened on load,
-// the arithmetic is f32 as the reference's). Per tile, wave w of a group of 4:
-//   S^T[32 keys][32 rows] over dims 32w .. 32w+31    16 MFMAs, A = K straight from HBM, B = Q (LDS)
+// keys in tiles of 32 positions. The arithmetic is f32, as the reference's, taken on the f16 matrix units: f32
+// operands are split into f16 hi + lo and each product is three v_mfma_f32_32x32x16_f16 passes (hi.hi + hi.lo +
+// lo.hi, f32 accumulation), two where one side is an f16 cache's K or V (exact in f16). Per tile, wave w of a group
+// of 4:
+//   S^T[32 keys][32 rows] over dims 32w .. 32w+31    2 dim steps, A = K straight from HBM, B = Q (split once, LDS)
 //   the four partial S^T summed through LDS in one order, exact-max online softmax (redundantly in every wave)
-//   O[32 rows][dims 32w .. 32w+31] += P . V           16 MFMAs, A = P (the S^T registers), B = V
+//   O[32 rows][dims 32w .. 32w+31] += P . V           2 key steps, A = P (split from the S^T registers), B = V
 // The 32x32 accumulator layout gives lane l (half s = l / 32) row l % 32 and keys 8a + 4s + b (register 4a + b), the
-// keys the A operand of the P.V MFMAs needs in that lane; with V stored in groups of 4 (f32) or 8 (f16) positions each
-// register quad's operand is one 16-byte (f32) or 8-byte (f16) load. Rows are positions modulo the ring: a 32-position
+// keys a 16-key step k of P.V takes in lane half s (16k + 4s + b and 16k + 8 + 4s + b: the order within a step is
+// free as long as P and V agree); with V stored in groups of 4 (f32) or 8 (f16) positions each register quad's keys
+// are one 16-byte (f32) or 8-byte (f16) load. Rows are positions modulo the ring: a 32-position
 // tile is one 32-row block (rings are multiples of 32), so a ring wrap only changes the tile's base address.
 // Each split writes one partial [m, l, 0, 0, acc[128]] per row; fl_merge adds the sink (as attn_fd_merge,
 // flint_attn.wgsl:241-257: the sink joins the maximum and the sum, never the output) and normalizes.
@@ -19,8 +22,6 @@
 namespace mkv {
 namespace flint {
 namespace {
-
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
 #ifndef FL_DEC_BUF
 #define FL_DEC_BUF 2      // decode: subtiles in registers per wave
@@ -33,11 +34,8 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 #endif
 
 constexpr int TILE = 32;
-constexpr int QPAD = HD + 4;  // LDS row of Q (floats)
+constexpr int QPAD = HD + 8;  // LDS row of Q's halves: 16-byte reads of 32 rows conflict-free
 
-__device__ inline f32x16 mfma32f(float a, float b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
 
 // Window start of the token at position p: the 513 positions up to p on sliding layers (lo_di, flint_attn.wgsl:82).
 __device__ inline int window_lo(int p, int win) { return win > 0 && p + 1 > win ? p + 1 - win : 0; }
@@ -45,12 +43,13 @@ __device__ inline int window_lo(int p, int win) { return win > 0 && p + 1 > win 
 template <int FMT>
 struct TileRegs;
 template <>
-struct TileRegs<1> {  // f32: K dims 32w + 8m + 4s .. +3 of key l % 32 (m < 4); V keys 8q + 4s .. +3 of dim 32w + l % 32
+struct TileRegs<1> {  // f32: K dims 32w + 16a + 8s + 4e .. +3 of key l % 32 (index 2a + e); V keys 8q + 4s .. +3 of
+                      // dim 32w + l % 32
     f32x4 k[4];
     f32x4 v[4];
 };
 template <>
-struct TileRegs<0> {  // f16: K dims 32w + 16a + 8s .. +7 (a < 2); V as f32, 4 halves
+struct TileRegs<0> {  // f16: K dims 32w + 16a + 8s .. +7 (a < 2); V keys 8q + 4s .. +3, 4 halves
     half8 k[2];
     half4 v[4];
 };
@@ -72,13 +71,20 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
     const int lo = max(cs, lo_first / TILE * TILE), hi = min(ce, pos0 + t0 + nt);  // keys [lo, hi) of this split
     const int ntile = hi > lo ? (hi - lo + TILE - 1) / TILE : 0;
 
-    __shared__ float qs[32][QPAD];
+    __shared__ __attribute__((aligned(16))) _Float16 qh[32][QPAD], ql[32][QPAD];  // Q split: hi, lo
     __shared__ f32x4 sx[2][NWG][4][4][64];  // partial S^T: [round parity][group][wave][register quad][lane]
-    for (int i = tid; i < 32 * HD / 4; i += 256 * NWG) {
-        const int row = i / (HD / 4), d4 = (i % (HD / 4)) * 4, t = t0 + (row >> 3);
-        f32x4 x = f32x4{};
-        if (t < T) x = *(const f32x4*)(q + ((size_t)t * QH + kvh * GQA + (row & 7)) * HD + d4);
-        *(f32x4*)&qs[row][d4] = x;
+    for (int i = tid; i < 32 * HD / 8; i += 256 * NWG) {
+        const int row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
+        f32x4 x0 = f32x4{}, x1 = f32x4{};
+        if (t < T) {
+            const float* qr = q + ((size_t)t * QH + kvh * GQA + (row & 7)) * HD + d8;
+            x0 = *(const f32x4*)qr;
+            x1 = *(const f32x4*)(qr + 4);
+        }
+        half8 hi, lo;
+        split8(x0, x1, hi, lo);
+        *(half8*)&qh[row][d8] = hi;
+        *(half8*)&ql[row][d8] = lo;
     }
     __syncthreads();
 
@@ -96,7 +102,7 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
 #pragma unroll
             for (int m = 0; m < 4; m++)
                 X.k[m] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       kr, b + ((8 * w + 2 * m + s) * TILE + r32) * 16, 0, LOAD_NT));
+                    kr, b + ((8 * w + 4 * (m >> 1) + 2 * s + (m & 1)) * TILE + r32) * 16, 0, LOAD_NT));
 #pragma unroll
             for (int qq = 0; qq < 4; qq++)
                 X.v[qq] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -119,22 +125,16 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
     auto step = [&](TileRegs<FMT>& X, int j) {
         const int k0 = lo + j * TILE;
         f32x16 S = f32x16{};
-        if constexpr (FMT == 1) {
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                const f32x4 qv = *(const f32x4*)&qs[r32][32 * w + 8 * m + 4 * s];
-#pragma unroll
-                for (int b = 0; b < 4; b++) S = mfma32f(X.k[m][b], qv[b], S);
-            }
-        } else {
-#pragma unroll
-            for (int a = 0; a < 2; a++) {
-                const f32x4 q0 = *(const f32x4*)&qs[r32][32 * w + 16 * a + 8 * s];
-                const f32x4 q1 = *(const f32x4*)&qs[r32][32 * w + 16 * a + 8 * s + 4];
-#pragma unroll
-                for (int b = 0; b < 4; b++) S = mfma32f((float)X.k[a][b], q0[b], S);
-#pragma unroll
-                for (int b = 0; b < 4; b++) S = mfma32f((float)X.k[a][4 + b], q1[b], S);
+        for (int a = 0; a < 2; a++) {  // dims 32w + 16a .. +15, lane half s: 8s .. 8s + 7
+            const half8 bh = *(const half8*)&qh[r32][32 * w + 16 * a + 8 * s];
+            const half8 bl = *(const half8*)&ql[r32][32 * w + 16 * a + 8 * s];
+            if constexpr (FMT == 1) {
+                half8 kh, kl;
+                split8(X.k[2 * a], X.k[2 * a + 1], kh, kl);
+                S = mfma3(kh, kl, bh, bl, S);
+            } else {
+                S = mfma2(X.k[a], bh, bl, S);
             }
         }
         const int pb = (j / NWG) & 1;
@@ -173,11 +173,6 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
 #pragma unroll
             for (int i = 0; i < 16; i++) O[i] *= __shfl(cf, 8 * (i >> 2) + 4 * s + (i & 3));
         }
-        float vv[4][4];
-#pragma unroll
-        for (int qq = 0; qq < 4; qq++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) vv[qq][b] = (float)X.v[qq][b];
         // positions outside [lo_first, hi) may be rows of other positions or never written: P is 0 there, and V
         // must not bring NaN in
         if (k0 < lo_first || k0 + TILE > hi) {
@@ -186,13 +181,26 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
                     const int key = k0 + 8 * qq + 4 * s + b;
-                    if (key < lo_first || key >= hi) vv[qq][b] = 0.f;
+                    if (key < lo_first || key >= hi) {
+                        if constexpr (FMT == 1) X.v[qq][b] = 0.f;
+                        else X.v[qq][b] = (_Float16)0.f;
+                    }
                 }
         }
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) O = mfma32f(sv[4 * qq + b], vv[qq][b], O);
+        for (int k = 0; k < 2; k++) {  // keys 16k + 4s + b (registers 8k + b) and 16k + 8 + 4s + b (8k + 4 + b)
+            half8 ph, pl;
+            split8(f32x4{sv[8 * k], sv[8 * k + 1], sv[8 * k + 2], sv[8 * k + 3]},
+                   f32x4{sv[8 * k + 4], sv[8 * k + 5], sv[8 * k + 6], sv[8 * k + 7]}, ph, pl);
+            if constexpr (FMT == 1) {
+                half8 vh, vl;
+                split8(X.v[2 * k], X.v[2 * k + 1], vh, vl);
+                O = mfma3(ph, pl, vh, vl, O);
+            } else {
+                const half8 vb = __builtin_shufflevector(X.v[2 * k], X.v[2 * k + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+                O = mfma32(pl, vb, mfma32(ph, vb, O));
+            }
+        }
     };
 
     // a ring of NBUF register tiles: round r computes slot r % NBUF after issuing the loads of round r + NBUF - 1
@@ -367,24 +375,23 @@ __global__ void __launch_bounds__(256) fl_rows(E* __restrict__ plane, size_t pla
 }
 
 
-// ---- one or two tokens: 16 query rows (token * 8 + head) on v_mfma_f32_16x16x4_f32 ----
+// ---- one or two tokens: 16 query rows (token * 8 + head) on the 16x16 f16 matrix units ----
 // Work-group (key split, kv head), 4 waves; each wave owns whole 16-position subtiles (w, w + 4, ...) over all 128
-// dims, so no per-tile exchange or barrier: S^T[16 keys][16 rows] is 32 MFMAs with A = K straight from HBM and B = Q
-// in registers, and P.V is 32 MFMAs with A = P (the S^T registers: lane l holds row l % 16 and keys 4g + r, g = l / 16,
-// register r) and B = V. The four waves' states are merged through LDS at the end; one partial per work-group.
-__device__ inline f32x4 mfma16f(float a, float b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
+// dims, so no per-tile exchange or barrier: S^T[16 keys][16 rows] is 4 dim steps of v_mfma_f32_16x16x32_f16 with
+// A = K straight from HBM and B = Q (split into f16 hi + lo once, in registers), and P.V is 8 dim blocks of
+// v_mfma_f32_16x16x16_f16 with A = P (split from the S^T registers: lane l holds row l % 16 and keys 4g + r,
+// g = l / 16, register r) and B = V. f32 operands take three passes (hi.hi + hi.lo + lo.hi), an f16 cache's K or V
+// two. The four waves' states are merged through LDS at the end; one partial per work-group.
 
 template <int FMT>
 struct SubRegs;
 template <>
-struct SubRegs<1> {  // f32: K dims 16a + 4g .. +3 of key l % 16 (a < 8); V keys 4g .. +3 of dim 16c + l % 16 (c < 8)
+struct SubRegs<1> {  // f32: K dims 32a + 8g + 4e .. +3 of key l % 16 (index 2a + e); V keys 4g .. +3 of dim 16c + l % 16
     f32x4 k[8];
     f32x4 v[8];
 };
 template <>
-struct SubRegs<0> {  // f16: K dims 32a + 8g .. +7 (a < 4); V as f32, 4 halves
+struct SubRegs<0> {  // f16: K dims 32a + 8g .. +7 (a < 4); V keys 4g .. +3 of dim 16c + l % 16, 4 halves
     half8 k[4];
     half4 v[8];
 };
@@ -402,17 +409,16 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
     const int lo = max(cs, lo_first / TILE * TILE), hi = min(ce, pos0 + T);
     const int nsub = hi > lo ? (hi - lo + 15) / 16 : 0;
 
-    // Q of the lane's row in registers, in the dim order of the K operands
-    float qv[32];
+    // Q of the lane's row in registers, split into f16 hi + lo: step a holds dims 32a + 8g .. +7 (the B operand)
+    half8 qh[4], ql[4];
     {
         const int t = r16 >> 3;
         const float* qr = q + ((size_t)t * QH + kvh * GQA + (r16 & 7)) * HD;
 #pragma unroll
-        for (int a = 0; a < 32 / 4; a++) {
-            const int d = FMT == 1 ? 16 * a + 4 * g : 32 * (a >> 1) + 8 * g + 4 * (a & 1);
-            const f32x4 x = t < T ? *(const f32x4*)(qr + d) : f32x4{};
-#pragma unroll
-            for (int b = 0; b < 4; b++) qv[4 * a + b] = x[b];
+        for (int a = 0; a < 4; a++) {
+            const f32x4 x0 = t < T ? *(const f32x4*)(qr + 32 * a + 8 * g) : f32x4{};
+            const f32x4 x1 = t < T ? *(const f32x4*)(qr + 32 * a + 8 * g + 4) : f32x4{};
+            split8(x0, x1, qh[a], ql[a]);
         }
     }
     const unsigned pbytes = (unsigned)(plane_elems * BPE);
@@ -430,7 +436,7 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
 #pragma unroll
             for (int a = 0; a < 8; a++)
                 X.k[a] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       kr, blk + ((4 * a + g) * 32 + sub + r16) * 16, 0, LOAD_NT));
+                    kr, blk + ((8 * (a >> 1) + 2 * g + (a & 1)) * 32 + sub + r16) * 16, 0, LOAD_NT));
 #pragma unroll
             for (int cc = 0; cc < 8; cc++)
                 X.v[cc] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -456,16 +462,18 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
     auto step = [&](SubRegs<FMT>& X, int j) {
         const int k0 = lo + 16 * j;
         f32x4 S = f32x4{};
-        if constexpr (FMT == 1) {
 #pragma unroll
-            for (int a = 0; a < 8; a++)
-#pragma unroll
-                for (int b = 0; b < 4; b++) S = mfma16f(X.k[a][b], qv[4 * a + b], S);
-        } else {
-#pragma unroll
-            for (int a = 0; a < 4; a++)
-#pragma unroll
-                for (int b = 0; b < 8; b++) S = mfma16f((float)X.k[a][b], qv[8 * a + b], S);
+        for (int a = 0; a < 4; a++) {
+            if constexpr (FMT == 1) {
+                half8 kh, kl;
+                split8(X.k[2 * a], X.k[2 * a + 1], kh, kl);
+                S = mfma16k32(kh, qh[a], S);
+                S = mfma16k32(kh, ql[a], S);
+                S = mfma16k32(kl, qh[a], S);
+            } else {
+                S = mfma16k32(X.k[a], qh[a], S);
+                S = mfma16k32(X.k[a], ql[a], S);
+            }
         }
         float sv[4];
         float mt = NEG_INF;
@@ -498,24 +506,33 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
                 for (int cc = 0; cc < 8; cc++) O[cc][r] *= f;
             }
         }
-        float vv[8][4];
-#pragma unroll
-        for (int cc = 0; cc < 8; cc++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) vv[cc][r] = (float)X.v[cc][r];
         if (k0 < lo_first || k0 + 16 > hi) {  // rows of other or unwritten positions: no NaN through V
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int key = k0 + 4 * g + r;
                 if (key < lo_first || key >= hi)
 #pragma unroll
-                    for (int cc = 0; cc < 8; cc++) vv[cc][r] = 0.f;
+                    for (int cc = 0; cc < 8; cc++) {
+                        if constexpr (FMT == 1) X.v[cc][r] = 0.f;
+                        else X.v[cc][r] = (_Float16)0.f;
+                    }
             }
         }
+        half4 ph, pl;
+        split4(f32x4{sv[0], sv[1], sv[2], sv[3]}, ph, pl);
 #pragma unroll
-        for (int cc = 0; cc < 8; cc++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) O[cc] = mfma16f(sv[r], vv[cc][r], O[cc]);
+        for (int cc = 0; cc < 8; cc++) {
+            if constexpr (FMT == 1) {
+                half4 vh, vl;
+                split4(X.v[cc], vh, vl);
+                O[cc] = mfma16k16(ph, vh, O[cc]);
+                O[cc] = mfma16k16(ph, vl, O[cc]);
+                O[cc] = mfma16k16(pl, vh, O[cc]);
+            } else {
+                O[cc] = mfma16k16(ph, X.v[cc], O[cc]);
+                O[cc] = mfma16k16(pl, X.v[cc], O[cc]);
+            }
+        }
     };
 
     const int mine = nsub > w ? (nsub - w + 3) / 4 : 0;  // this wave's subtiles w, w + 4, ...

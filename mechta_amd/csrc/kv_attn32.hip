@@ -33,20 +33,6 @@ constexpr int TILE = 32;                       // keys per tile: one K block, ei
 constexpr unsigned TILE_BYTES = TILE * HD * 4;  // 32 KB of each plane
 constexpr int QPAD = HD + 8;                   // LDS row of Q's halves: 16-byte reads of 32 rows conflict-free
 
-// x = hi + lo to 2^-22: hi = f16(x), lo = f16(x - hi) (the residual is exact in f32)
-__device__ inline void split8(f32x4 a, f32x4 b, half8& hi, half8& lo) {
-    hi = half8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
-               (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
-    lo = half8{(_Float16)(a.x - (float)hi[0]), (_Float16)(a.y - (float)hi[1]), (_Float16)(a.z - (float)hi[2]),
-               (_Float16)(a.w - (float)hi[3]), (_Float16)(b.x - (float)hi[4]), (_Float16)(b.y - (float)hi[5]),
-               (_Float16)(b.z - (float)hi[6]), (_Float16)(b.w - (float)hi[7])};
-}
-// c += a.b with a = ah + al, b = bh + bl: three f16 MFMAs (al.bl dropped)
-__device__ inline f32x16 mfma3(half8 ah, half8 al, half8 bh, half8 bl, f32x16 c) {
-    c = mfma32(ah, bh, c);
-    c = mfma32(ah, bl, c);
-    return mfma32(al, bh, c);
-}
 __device__ inline f32x4 bload4f(rsrc_t r, unsigned off) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, LOAD_NT));
 }

@@ -5,6 +5,7 @@
 namespace mkv {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
@@ -24,6 +25,38 @@ __device__ inline f32x16 mfma32(half8 a, half8 b, f32x16 c) {
 
 __device__ inline f32x4 mfma16(half8 a, half8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// f32 products on the f16 matrix units. An f32 operand x is split into hi = f16(x) and lo = f16(x - hi) (the residual
+// is exact in f32), and a product a.b is taken as hi(a)hi(b) + hi(a)lo(b) + lo(a)hi(b) with f32 accumulation: the
+// dropped lo(a)lo(b) is below 2^-22 of |a||b|. Operands that are f16 already (an f16 cache's K or V) need two passes.
+// x = hi + lo to 2^-22: hi = f16(x), lo = f16(x - hi) (the residual is exact in f32)
+__device__ inline void split8(f32x4 a, f32x4 b, half8& hi, half8& lo) {
+    hi = half8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+               (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+    lo = half8{(_Float16)(a.x - (float)hi[0]), (_Float16)(a.y - (float)hi[1]), (_Float16)(a.z - (float)hi[2]),
+               (_Float16)(a.w - (float)hi[3]), (_Float16)(b.x - (float)hi[4]), (_Float16)(b.y - (float)hi[5]),
+               (_Float16)(b.z - (float)hi[6]), (_Float16)(b.w - (float)hi[7])};
+}
+// c += a.b with a = ah + al, b = bh + bl: three f16 MFMAs (al.bl dropped)
+__device__ inline f32x16 mfma3(half8 ah, half8 al, half8 bh, half8 bl, f32x16 c) {
+    c = mfma32(ah, bh, c);
+    c = mfma32(ah, bl, c);
+    return mfma32(al, bh, c);
+}
+__device__ inline half4 f16x4(f32x4 a) { return half4{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w}; }
+__device__ inline void split4(f32x4 a, half4& hi, half4& lo) {
+    hi = f16x4(a);
+    lo = half4{(_Float16)(a.x - (float)hi[0]), (_Float16)(a.y - (float)hi[1]), (_Float16)(a.z - (float)hi[2]),
+               (_Float16)(a.w - (float)hi[3])};
+}
+// c += a.(bh + bl) with a exact in f16: two passes
+__device__ inline f32x16 mfma2(half8 a, half8 bh, half8 bl, f32x16 c) { return mfma32(a, bl, mfma32(a, bh, c)); }
+__device__ inline f32x4 mfma16k32(half8 a, half8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ inline f32x4 mfma16k16(half4 a, half4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
 // Key offset inside a 32-key K block of the key loaded by A-operand row m of the 32x32 MFMA. The C layout of that
