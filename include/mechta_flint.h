@@ -9,8 +9,9 @@
  * query head's sink logit joins the softmax maximum and sum but not the output (flint_attn.wgsl:1-8, 241-257).
  *
  * Layout: per (layer, K|V, kv head) one plane of rows x 128 elements. f32: K [row/32][d/4][row%32][4], V [row/4][d]
- * [row%4]; f16: K [row/32][d/8][row%32][8], V [row/8][d][row%8] -- the operand layouts of the CDNA4 fp32 matrix
- * instructions (f16 values are widened on load; all attention arithmetic is f32, as the reference's). mfl_read_rows /
+ * [row%4]; f16: K [row/32][d/8][row%32][8], V [row/8][d][row%8] -- the operand layouts of the CDNA4 matrix
+ * instructions. Attention arithmetic is f32-class, as the reference's f32: products run on the f16 matrix units with
+ * f32 operands split into f16 hi + lo (hi.hi + hi.lo + lo.hi, f32 accumulation; within 1e-5 of exact f32). mfl_read_rows /
  * mfl_write_rows convert to and from the reference's row layout [row][kvh][128] (flint_attn.wgsl:3, kv_put).
  *
  * All calls are ordered on the handle's stream; device pointers are plain HIP device addresses.

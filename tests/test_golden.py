@@ -2,7 +2,7 @@
 
 CPU: the input generator is pinned by the published SplitMix64 vectors and by its distribution, and the oracle still
 reproduces every stored output. GPU: the HIP path, through the C ABI, matches the stored outputs: appended rows and
-row hashes bit-exact, attention within max-abs 2e-3 / relative 1e-3 (Flint: 1e-5 / 1e-5, f32 arithmetic).
+row hashes bit-exact, attention within max-abs 2e-3 / relative 1e-3 (Flint: 1e-5 / 1e-5, f32-class arithmetic).
 """
 import hashlib
 import os

@@ -1,8 +1,8 @@
 """GPU parity tests of the Flint KV path (include/mechta_flint.h) through the C ABI, against the CPU oracle
 (oracle/flint_oracle.c).
 
-Bars: ring writes, row conversion, RoPE and photo bit-exact; attention (f32 arithmetic on f32 or f16 caches, as the
-reference's) within max-abs 1e-5 and relative (Frobenius) 1e-5 of attn_fd + attn_fd_merge (one token) or attn_pf (a
+Bars: ring writes, row conversion, RoPE and photo bit-exact; attention (f32-class arithmetic on f32 or f16 caches, as
+the reference's f32: f16 matrix products of split f32 operands) within max-abs 1e-5 and relative (Frobenius) 1e-5 of attn_fd + attn_fd_merge (one token) or attn_pf (a
 block), with sinks, windows and ring wraps.
 """
 import numpy as np
