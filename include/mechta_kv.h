@@ -100,7 +100,8 @@ int mkv_set_len(mkv_t* h, int len);
  *             out = attention * sigmoid(qf[h*512 + 256 + d]) (attn_gate, ops.wgsl:171-177).
  * Requires n + ntok - 1 <= len(layer). Replaces attn_fd (ops.wgsl:310-394), q_dmx + attn_dmx2 (dmx.rs:19-138) and
  * attn_fd_combine (ops.wgsl:523-538). f16 store: Q and P rounded to f16 for the matrix units, f32 sums (as attn_dmx);
- * f32 store: f32 throughout (as attn_fd). */
+ * f32 store: f32-class throughout (as attn_fd; products on the f16 matrix units from f32 operands split into f16
+ * hi + lo, within 1e-5 of exact f32). */
 int mkv_decode(mkv_t* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
                const float* gate_src);
 
