@@ -560,11 +560,13 @@ __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part,
 
 DecodePlan decode_plan(int n, int ntok, int start) {
     // 64-position stages dealt round robin (neighbouring stages stream from different CUs at once, which keeps HBM
-    // busier than one contiguous range per work-group), at least 2 stages and at most DEC_WG work-groups per kv head
+    // busier than one contiguous range per work-group), at most DEC_WG work-groups per kv head; a short context gets
+    // one stage per work-group (all its loads in flight at once: 1 token at 4,097 positions 10.7 us per step against
+    // 11.0 us with at least 2 stages each)
     const int kend = n + ntok - 1;
     const int s0 = start / KPS_F16 * KPS_F16;
     const int nu = (kend - s0 + KPS_F16 - 1) / KPS_F16;
-    int g = nu / 2;
+    int g = nu;
     g = g < 1 ? 1 : g > DEC_WG ? DEC_WG : g;
     return DecodePlan{0, g, 0, s0, nu};
 }

@@ -3,6 +3,7 @@
 // The store replaces the reference's per-layer K/V wgpu buffers (engine.rs:493-496) and the host side of the
 // dispatches that touch them (uniform writes engine.rs:618-673, quad.rs:277-289, engine.rs:902-931; root I/O
 // engine.rs:782-823). Argument checks return the error codes of the header where the reference panics.
+#include <algorithm>
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -152,7 +153,7 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
         (void)hipGetLastError();
         return fail(MKV_E_NOMEM, "mkv_create: hipMalloc of %zu bytes failed", bytes);
     }
-    h->dws.max_chunks = ctx / 128 + 2;
+    h->dws.max_chunks = std::min(ctx / 64 + 2, 128);  // decode splits: one per 64-position stage, at most 124
     size_t dws_bytes = (size_t)KVH * ROWS * h->dws.max_chunks * PART * sizeof(float);
     e = hipMalloc(&h->dws.part, dws_bytes);
     if (e != hipSuccess) {
