@@ -48,7 +48,9 @@ template <int NWG, int NBUF>
 __global__ void __launch_bounds__(256 * NWG) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
                                                 size_t plane_elems, const float* __restrict__ q, int T, int n,
                                                 int start, float scale2, int span, int nch, int c0, int nrb, int rpk,
-                                                float* __restrict__ part) {
+                                                float* __restrict__ part, const float* __restrict__ akn,
+                                                const float* __restrict__ av, const float* __restrict__ atab, int apos,
+                                                int antok) {
     // XCD-aware order: consecutive work-groups go round robin to the 8 XCDs, so work item W = (L % 8) (G / 8) + L / 8
     // puts the token blocks that stream the same keys on one XCD's L2
     const int G = gridDim.x, L = blockIdx.x;
@@ -75,6 +77,26 @@ __global__ void __launch_bounds__(256 * NWG) attn_f32(const float* __restrict__ 
         lo = lo0 + c * TILE;
         ntile = c < nt_all ? (nt_all - c + nch - 1) / nch : 0;
         tstep = nch;
+    }
+
+    // Fused append (decode only: mkv_append_decode on the f32 store). The new rows [apos, apos + antok) lie in the
+    // last one or two tiles; the work-group holding a tile computes its new rows here (the same arithmetic as
+    // append_kernel) into LDS, patches them into that tile's K and V registers, and stores them to the planes after
+    // its loop: no load waits for the stores, and no other work-group reads those positions in this launch.
+    __shared__ __attribute__((aligned(16))) float newk[4][HD], newv[4][HD];
+    int apf = 0, apl = 0;  // this work-group's new rows [apf, apl)
+    if (antok > 0) {
+        const int lo0 = start / TILE * TILE;
+        for (int p = apos; p < apos + antok; p++)
+            if (((p - lo0) / TILE) % nch == c) {
+                apf = apl == 0 ? p : apf;
+                apl = p + 1;
+            }
+        for (int i = tid; i < (apl - apf) * HD; i += 256 * NWG) {
+            const int t = apf - apos + i / HD, d = i % HD;
+            newk[i / HD][d] = rope_dim(akn + ((size_t)t * KVH + kvh) * HD, atab + (size_t)t * 64, d);
+            newv[i / HD][d] = av[(size_t)t * (KVH * HD) + kvh * HD + d];
+        }
     }
 
     __shared__ __attribute__((aligned(16))) _Float16 qh[ROWS][QPAD], ql[ROWS][QPAD];  // Q split: hi, lo
@@ -115,6 +137,21 @@ __global__ void __launch_bounds__(256 * NWG) attn_f32(const float* __restrict__ 
     f32x16 O[2] = {f32x16{}, f32x16{}};
     auto step = [&](Tile& X, int j) {
         const int k0 = lo + j * tstep * TILE;
+        if (k0 < apl && k0 + TILE > apf) {  // the tile holds new rows: their K and V from LDS
+            const int key = k0 + r32;
+            if (key >= apf && key < apl) {
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    X.k[i] = *(const f32x4*)&newk[key - apf][64 * w + 16 * (i >> 1) + 8 * s + 4 * (i & 1)];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int kv = k0 + 16 * (i >> 2) + 8 * (i & 1) + 4 * s + b;
+                    if (kv >= apf && kv < apl) X.v[i][b] = newv[kv - apf][64 * w + 32 * ((i >> 1) & 1) + r32];
+                }
+        }
         f32x16 S = f32x16{};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -204,6 +241,17 @@ __global__ void __launch_bounds__(256 * NWG) attn_f32(const float* __restrict__ 
         }
     }
 
+    // the fused append's rows into the planes, for the launches that follow
+    if (apl > apf) {
+        float* Kp = (float*)kplane + (size_t)kvh * plane_elems;
+        float* Vp = (float*)vplane + (size_t)kvh * plane_elems;
+        for (int i = tid; i < (apl - apf) * HD; i += 256 * NWG) {
+            const int r = i / HD, d = i % HD;
+            Kp[k_off32(apf + r, d)] = newk[r][d];
+            Vp[v_off32(apf + r, d)] = newv[r][d];
+        }
+    }
+
     // merge group 1 into group 0 through LDS (the parity buffers are free after the barrier)
     if constexpr (NWG == 2) {
         __syncthreads();
@@ -280,7 +328,9 @@ Attn32Plan attn32_plan(int T, int n, int start) {
 }
 
 hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
-                           float scale, const Attn32Plan& p, int rpk, float* part, const Launch& L) {
+                           float scale, const Attn32Plan& p, int rpk, float* part, const FusedAppend& fa,
+                           const Launch& L) {
+    if (fa.ntok > 0 && (p.span != 0 || fa.ntok > 4)) return hipErrorInvalidValue;  // fused append: decode plans only
     if (g.fmt != 1) return hipErrorNotSupported;
     const char* b = (const char*)base;
     const float* kp = (const float*)(b + g.plane(layer, 0, 0) * g.plane_bytes());
@@ -288,9 +338,9 @@ hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const flo
     dim3 grid(p.nrb * (p.nch - p.c0) * KVH);
     if (T <= 4)
         return launch(attn_f32<1, 2>, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
-                      p.nch, p.c0, p.nrb, rpk, part);
+                      p.nch, p.c0, p.nrb, rpk, part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
     return launch(attn_f32<2, 2>, grid, dim3(512), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
-                  p.nch, p.c0, p.nrb, rpk, part);
+                  p.nch, p.c0, p.nrb, rpk, part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
 }
 
 }  // namespace mkv

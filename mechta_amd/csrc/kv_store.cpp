@@ -79,7 +79,7 @@ hipError_t decode_all(mkv_store* h, int layer, const float* q, int ntok, int n, 
         const Attn32Plan p = attn32_plan(ntok, n, start);
         if (p.nch > h->dws.max_chunks) return hipErrorInvalidValue;
         hipError_t e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
-            return launch_attn_f32(h->g, h->base, layer, q, ntok, n, start, scale, p, ROWS, h->dws.part, L);
+            return launch_attn_f32(h->g, h->base, layer, q, ntok, n, start, scale, p, ROWS, h->dws.part, fa, L);
         });
         if (e != hipSuccess) return e;
         return traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {
@@ -276,10 +276,6 @@ int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* kn, con
     if (pos > h->len[layer])
         return fail(MKV_E_POS, "mkv_append_decode: position %d leaves a hole after the written length %d", pos,
                     h->len[layer]);
-    if (h->g.fmt != MKV_F16) {  // f32 store: the append kernel, then the decode
-        if (int rc = mkv_append(h, layer, pos, ntok, kn, v, tab)) return rc;
-        return mkv_decode(h, layer, q, ntok, n, start, scale, out, gate);
-    }
     const int old_len = h->len[layer];
     h->len[layer] = pos + ntok;
     if (int rc = check_attn(h, "mkv_append_decode", layer, q, ntok, 4, n, start, out)) {
@@ -323,7 +319,7 @@ int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, fl
         if (!prefill_ws(h, need, e))
             return fail(MKV_E_NOMEM, "mkv_prefill: %zu bytes of split-K partials", need * sizeof(float));
         e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
-            return launch_attn_f32(h->g, h->base, layer, q, T, n, start, scale, p, T * GQA, h->pws, L);
+            return launch_attn_f32(h->g, h->base, layer, q, T, n, start, scale, p, T * GQA, h->pws, FusedAppend{}, L);
         });
         if (e == hipSuccess)
             e = traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {

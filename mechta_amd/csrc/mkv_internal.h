@@ -165,7 +165,8 @@ struct Attn32Plan {
 };
 Attn32Plan attn32_plan(int T, int n, int start);
 hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
-                           float scale, const Attn32Plan& p, int rpk, float* part, const Launch& L);
+                           float scale, const Attn32Plan& p, int rpk, float* part, const FusedAppend& fa,
+                           const Launch& L);
 // Prefill (f16 store): split-K pass into the partials ws, then launch_merge with the returned plan.
 struct PrefillPlan {
     int span, nch;  // splits of [0, span) as chunk_lo

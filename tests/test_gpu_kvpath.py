@@ -203,19 +203,20 @@ def test_decode_gate(torch_gpu, mk):
     assert_attn_close(out, ref, what="gated")
 
 
+@pytest.mark.parametrize("fmt", [F16, F32])
 @pytest.mark.parametrize("ctx,n0", [(4096, 1234), (4096, 1279), (4096, 1282), (4096, 66), (20480, 19199),
                                     (66560, 65536 + 63)])
-def test_append_decode_fused_entry(torch_gpu, mk, ctx, n0):
-    """The fused entry equals append + decode bit for bit, also when the new rows straddle two 64-key stages (held
-    by different work-groups) or sit in a work-group's first stages."""
+def test_append_decode_fused_entry(torch_gpu, mk, ctx, n0, fmt):
+    """The fused entry equals append + decode bit for bit, also when the new rows straddle two 64-key stages (f16) or
+    32-key tiles (f32) held by different work-groups, or sit in a work-group's first stages."""
     torch = torch_gpu
-    print(f"fused append+decode ctx={ctx} n0={n0}", flush=True)
+    print(f"fused append+decode fmt={fmt} ctx={ctx} n0={n0}", flush=True)
     kn, v = kv_inputs(31, 4)
     tab = O.rope_tables(n0 - 1, 4)
     q = q_inputs(32, 4)
-    with mk.KvStore(1, ctx, F16) as a, mk.KvStore(1, ctx, F16) as b:
-        fill(torch, a, 0, F16, n0 - 1, seed=33)
-        fill(torch, b, 0, F16, n0 - 1, seed=33)
+    with mk.KvStore(1, ctx, fmt) as a, mk.KvStore(1, ctx, fmt) as b:
+        fill(torch, a, 0, fmt, n0 - 1, seed=33)
+        fill(torch, b, 0, fmt, n0 - 1, seed=33)
         oa = a.append_decode(0, n0, dev(torch, kn), dev(torch, v), dev(torch, tab), dev(torch, q)).cpu().numpy()
         b.append(0, n0 - 1, dev(torch, kn), dev(torch, v), dev(torch, tab))
         ob = b.decode(0, dev(torch, q), n0).cpu().numpy()
@@ -223,7 +224,10 @@ def test_append_decode_fused_entry(torch_gpu, mk, ctx, n0):
         kb, vb = caches_np(b, 0, n0 + 3)
     assert np.array_equal(ka, kb) and np.array_equal(va, vb), "fused append wrote other rows"
     assert np.array_equal(oa, ob)
-    assert_attn_close(oa, O.attn_dmx(ka, va, q, n0), what="fused vs oracle")
+    if fmt == F16:
+        assert_attn_close(oa, O.attn_dmx(ka, va, q, n0), what="fused vs oracle")
+    else:
+        assert_attn_close(oa, O.attn_fd(F32, ka, va, q, n0), atol=1e-5, rtol=1e-5, what="fused f32 vs oracle")
 
 
 # ------------------------------------------------------------------------------------------------ prefill --------
