@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="no GPU work: summarize two rocprofv3 --pmc output directories (FETCH_SIZE, WRITE_SIZE) of a "
                          "--calib-copy run into HBM bytes per dispatch")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="no GPU work: group a rocprofv3 --kernel-trace csv by kernel and grid (launches, mean, median, "
+                         "min, max microseconds) as a markdown table")
     return ap.parse_args()
 
 
@@ -50,6 +53,23 @@ def parse():
 # (rocprofv3 --pmc of "bench.py --steps 20 --warmup 2 --no-cpu --no-extra --calib-copy", summarized by --pmc-summary; the
 # counters are scaled by what they read for the 256 MiB copy of --calib-copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).
 TRAFFIC = {"decode_f16": 143.54e6, "prefill_f16": 174.96e6}
+
+
+def trace_summary(path):
+    """Per (kernel, grid, work-group size) of a rocprofv3 kernel trace: launches and durations in microseconds."""
+    import csv
+    import collections
+    import statistics
+    per = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:90]
+        key = (name, r.get("Grid_Size_X", r.get("Grid_Size")), r.get("Workgroup_Size_X", r.get("Workgroup_Size")))
+        per[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000)
+    print("| kernel | grid threads | wg | launches | mean us | median us | min us | max us |")
+    print("|---|---|---|---|---|---|---|---|")
+    for (name, grid, wg), v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| {name} | {grid} | {wg} | {len(v)} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} | "
+              f"{min(v):.2f} | {max(v):.2f} |")
 
 
 def pmc_summary(fetch_dir, write_dir):
@@ -422,6 +442,9 @@ def main():
     args = parse()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the KV-cache path would "
