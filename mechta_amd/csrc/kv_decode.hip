@@ -30,10 +30,6 @@ constexpr int KPS = KPS_F16;                   // keys per stage of the decode r
 #define MKV_DEC_WG 124
 #endif
 constexpr int DEC_WG = MKV_DEC_WG;             // most work-groups per kv head (2 x 124 on the 256 CUs)
-#ifndef MKV_DEC_NSET
-#define MKV_DEC_NSET 0
-#endif
-constexpr int DEC_NSET = MKV_DEC_NSET;         // register sets of the decode pipeline; 0 = staggered K / V streams
 constexpr int PS_STRIDE = KPS + 8;             // halves per P row in LDS (conflict-free 16-byte reads)
 constexpr int QS_STRIDE = HD + 8;              // halves per Q row in LDS
 constexpr int NEWMAX = 4;                      // appended rows per call
@@ -46,9 +42,8 @@ struct StageRegs {
     half8 v[4];
 };
 
-// NSET register sets of stage operands (2 to 4): NSET - 1 stages in flight ahead of the one computed; NSET = 0:
-// K two stages ahead and V one stage ahead in two sets each.
-template <int NSET>
+// Stage operands in four register sets: K two stages ahead and V one stage ahead, two sets each (three or four
+// sets of whole stages, two or three stages in flight, measured slower).
 __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane, _Float16* __restrict__ vplane,
                                                   size_t plane_elems, const float* __restrict__ q, int ntok, int n,
                                                   int start, float scale2, int s0, int nu,
@@ -112,10 +107,6 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
 #pragma unroll
         for (int s2 = 0; s2 < 4; s2++) R.v[s2] = bload16(vr, vofs + s2 * (2 * VGRP * HD * 2));
     };
-    auto load = [&](int j, StageRegs& R) {
-        load_k(j, R);
-        load_v(j, R);
-    };
     // Fused append (mkv_append_decode). The new rows [apf, apl) of the stages this work-group owns (at most two
     // stages hold new rows) are computed into LDS (the same arithmetic as append_kernel) and patched into the K and V
     // registers of the stage that holds them, so no load waits for their stores; they are stored to the planes
@@ -154,23 +145,13 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     }
     // three stages in flight from the start; loads of stages past this work-group's last are out of range and move
     // no bytes, so no load is behind a branch (a branch around loads makes the compiler's wait counts pessimistic)
-    StageRegs R0, R1, R2, R3;
-    if constexpr (NSET == 0) {  // staggered streams: K two stages ahead, V one (R0/R1 hold K, R2/R3 hold V)
-        load_k(0, R0);
-        load_k(1, R1);
-        load_v(0, R2);
-    } else {
-        load(0, R0);
-        if constexpr (NSET > 2) load(1, R1);
-        if constexpr (NSET > 3) load(2, R2);
-    }
+    StageRegs R0, R1, R2, R3;  // staggered streams: K two stages ahead, V one (R0/R1 hold K, R2/R3 hold V)
+    load_k(0, R0);
+    load_k(1, R1);
+    load_v(0, R2);
     if (nr > 0) {
-        // the direct loads precede the 4 Q and the stage loads; then every wave's LDS data is in
-        static_assert(NSET == 0 || (NSET >= 2 && NSET <= 4), "wait counts below");
-        if constexpr (NSET == 0) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-        if constexpr (NSET == 2) asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
-        if constexpr (NSET == 3) asm volatile("s_waitcnt vmcnt(20)\n\ts_barrier" ::: "memory");
-        if constexpr (NSET == 4) asm volatile("s_waitcnt vmcnt(28)\n\ts_barrier" ::: "memory");
+        // the direct loads precede the 4 Q loads and the 12 stage loads; then every wave's LDS data is in
+        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
         for (int it = tid; it < nr * HD; it += 512) {
             const int i = it / HD, d = it % HD;
             newk[i][d] = __builtin_bit_cast(_Float16, f2h(rope_dim(aink + i * HD, aint + i * 64, d)));
@@ -299,23 +280,24 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
         for (int s2 = 0; s2 < KPS / 16; s2++) O = mfma32(pa[s2], vb[s2], O);
     };
 
-    // Software pipeline, one barrier per stage. Iteration j: issue the loads of stage j + NSET - 1, the S MFMAs of
-    // stage j + 1 (they run while the VALU does the softmax of stage j, whose S the previous iteration left in LDS),
-    // store S of j + 1, barrier, then P.V of stage j. Buffers alternate by stage parity; a buffer is rewritten two
-    // stages after it was read, behind the barrier between. Register sets rotate with period NSET: stage j's V is in
-    // R[j % NSET], stage j + 1's K in R[(j + 1) % NSET], and stage j + NSET - 1 loads into R[(j - 1) % NSET].
-    auto iter = [&](int j, const StageRegs& Rj, const StageRegs& Rj1, StageRegs& Rjn, auto has_next) {
+    // Software pipeline, one barrier per stage. Iteration j: issue the loads of K for stage j + 2 and of V for stage
+    // j + 1, the S MFMAs of stage j + 1 (K loaded one iteration ago; they run while the VALU does the softmax of stage
+    // j, whose S the previous iteration left in LDS), store S of j + 1, barrier, then P.V of stage j (V loaded one
+    // iteration ago): about one stage of bytes in flight, each operand a whole iteration ahead. Buffers alternate by
+    // stage parity; a buffer is rewritten two stages after it was read, behind the barrier between.
+    auto iter2 = [&](int j, StageRegs& Kn, const StageRegs& K1, StageRegs& Vn, const StageRegs& V0, auto has_next) {
         const int buf = j & 1;
-        load(j + NSET - 1, Rjn);
+        load_k(j + 2, Kn);
+        load_v(j + 1, Vn);
         if constexpr (decltype(has_next)::value) {
-            auto store_s = s_part(j + 1, Rj1, buf ^ 1);
+            auto store_s = s_part(j + 1, K1, buf ^ 1);
             softmax(j, buf);
             store_s();
         } else {
             softmax(j, buf);
         }
         lds_barrier();
-        pv(j, buf, Rj);
+        pv(j, buf, V0);
     };
     if (nst > 0) {
         s_part(0, R0, 0)();
@@ -324,85 +306,15 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     using T = std::true_type;
     using F = std::false_type;
     int j = 0;
-    if constexpr (NSET == 0) {
-        // iteration j: K of stage j + 2 and V of stage j + 1 load; S of j + 1 (K loaded one iteration ago); P.V of
-        // j (V loaded one iteration ago): one stage of bytes in flight, each operand a whole iteration ahead
-        auto iter2 = [&](int j, StageRegs& Kn, const StageRegs& K1, StageRegs& Vn, const StageRegs& V0, auto has_next) {
-            const int buf = j & 1;
-            load_k(j + 2, Kn);
-            load_v(j + 1, Vn);
-            if constexpr (decltype(has_next)::value) {
-                auto store_s = s_part(j + 1, K1, buf ^ 1);
-                softmax(j, buf);
-                store_s();
-            } else {
-                softmax(j, buf);
-            }
-            lds_barrier();
-            pv(j, buf, V0);
-        };
-        for (; j + 2 < nst; j += 2) {
-            iter2(j, R0, R1, R3, R2, T{});
-            iter2(j + 1, R1, R0, R2, R3, T{});
-        }
-        if (nst - j == 1) {
-            iter2(j, R0, R1, R3, R2, F{});
-        } else if (nst - j == 2) {
-            iter2(j, R0, R1, R3, R2, T{});
-            iter2(j + 1, R1, R0, R2, R3, F{});
-        }
-    } else if constexpr (NSET == 4) {
-        for (; j + 5 <= nst; j += 4) {
-            iter(j, R0, R1, R3, T{});
-            iter(j + 1, R1, R2, R0, T{});
-            iter(j + 2, R2, R3, R1, T{});
-            iter(j + 3, R3, R0, R2, T{});
-        }
-        const int rem = nst - j;  // the last 1 to 4 stages, straight-line
-        if (rem == 1) {
-            iter(j, R0, R1, R3, F{});
-        } else if (rem == 2) {
-            iter(j, R0, R1, R3, T{});
-            iter(j + 1, R1, R2, R0, F{});
-        } else if (rem == 3) {
-            iter(j, R0, R1, R3, T{});
-            iter(j + 1, R1, R2, R0, T{});
-            iter(j + 2, R2, R3, R1, F{});
-        } else if (rem == 4) {
-            iter(j, R0, R1, R3, T{});
-            iter(j + 1, R1, R2, R0, T{});
-            iter(j + 2, R2, R3, R1, T{});
-            iter(j + 3, R3, R0, R2, F{});
-        }
-    } else if constexpr (NSET == 3) {
-        for (; j + 4 <= nst; j += 3) {
-            iter(j, R0, R1, R2, T{});
-            iter(j + 1, R1, R2, R0, T{});
-            iter(j + 2, R2, R0, R1, T{});
-        }
-        const int rem = nst - j;  // the last 1 to 3 stages, straight-line
-        if (rem == 1) {
-            iter(j, R0, R1, R2, F{});
-        } else if (rem == 2) {
-            iter(j, R0, R1, R2, T{});
-            iter(j + 1, R1, R2, R0, F{});
-        } else if (rem == 3) {
-            iter(j, R0, R1, R2, T{});
-            iter(j + 1, R1, R2, R0, T{});
-            iter(j + 2, R2, R0, R1, F{});
-        }
-    } else {
-        for (; j + 3 <= nst; j += 2) {
-            iter(j, R0, R1, R1, T{});
-            iter(j + 1, R1, R0, R0, T{});
-        }
-        const int rem = nst - j;  // the last 1 or 2 stages, straight-line
-        if (rem == 1) {
-            iter(j, R0, R1, R1, F{});
-        } else if (rem == 2) {
-            iter(j, R0, R1, R1, T{});
-            iter(j + 1, R1, R0, R0, F{});
-        }
+    for (; j + 2 < nst; j += 2) {
+        iter2(j, R0, R1, R3, R2, T{});
+        iter2(j + 1, R1, R0, R2, R3, T{});
+    }
+    if (nst - j == 1) {
+        iter2(j, R0, R1, R3, R2, F{});
+    } else if (nst - j == 2) {
+        iter2(j, R0, R1, R3, R2, T{});
+        iter2(j + 1, R1, R0, R2, R3, F{});
     }
 
     // the appended rows into the planes, for the launches that follow (stores issued here, behind no loads)
@@ -580,7 +492,7 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
     void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
     const float scale2 = scale * LOG2E;
     if (g.fmt != 0) return hipErrorNotSupported;
-    return launch(decode_f16<DEC_NSET>, dim3(p.nch, KVH), dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2,
+    return launch(decode_f16, dim3(p.nch, KVH), dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2,
                   p.s0, p.nu, ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
 }
 
