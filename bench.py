@@ -488,7 +488,7 @@ def main():
                      "kernel": "decode_f16", "bytes_per_launch": int(core_bytes)},
     }
     if not args.no_prefill:
-        pf = bench_prefill(torch, mk, max(3, args.steps // 20), 2)
+        pf = bench_prefill(torch, mk, max(10, args.steps // 5), 5)
         res["prefill_tok_s"] = round(pf["tok_s"], 1)
         res["prefill_ms"] = round(pf["ms"], 4)
         if pf["core_launches"] == 1:
