@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="no GPU work: summarize two rocprofv3 --pmc output directories (FETCH_SIZE, WRITE_SIZE) of a "
                          "--calib-copy run into HBM bytes per dispatch")
+    ap.add_argument("--counter-summary", metavar="PMC_DIR",
+                    help="no GPU work: mean of every counter per kernel and grid of a rocprofv3 --pmc output directory, "
+                         "as a markdown table")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="no GPU work: group a rocprofv3 --kernel-trace csv by kernel and grid (launches, mean, median, "
                          "min, max microseconds) as a markdown table")
@@ -53,6 +56,27 @@ def parse():
 # (rocprofv3 --pmc of "bench.py --steps 20 --warmup 2 --no-cpu --no-extra --calib-copy", summarized by --pmc-summary; the
 # counters are scaled by what they read for the 256 MiB copy of --calib-copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).
 TRAFFIC = {"decode_f16": 143.54e6, "prefill_f16": 174.96e6}
+
+
+def counter_summary(d):
+    """Mean value per dispatch of each collected counter, per (kernel, grid) of a rocprofv3 --pmc directory."""
+    import csv
+    import glob
+    import collections
+    f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)[0]
+    per = collections.defaultdict(lambda: collections.defaultdict(list))
+    for r in csv.DictReader(open(f)):
+        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:60]
+        if "mkv" not in name:
+            continue
+        per[(name, int(r["Grid_Size"]))][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    names = sorted({c for v in per.values() for c in v})
+    print("| kernel | grid | dispatches | " + " | ".join(names) + " |")
+    print("|---|---|---|" + "---|" * len(names))
+    for (name, grid), cs in sorted(per.items()):
+        n = max(len(v) for v in cs.values())
+        vals = " | ".join(f"{sum(cs[c]) / len(cs[c]):.0f}" if c in cs else "" for c in names)
+        print(f"| {name} | {grid} | {n} | {vals} |")
 
 
 def trace_summary(path):
@@ -442,6 +466,9 @@ def main():
     args = parse()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.counter_summary:
+        counter_summary(args.counter_summary)
         return
     if args.trace_summary:
         trace_summary(args.trace_summary)
