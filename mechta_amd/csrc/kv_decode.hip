@@ -34,7 +34,7 @@ constexpr int PS_STRIDE = KPS + 8;             // halves per P row in LDS (confl
 constexpr int QS_STRIDE = HD + 8;              // halves per Q row in LDS
 constexpr int NEWMAX = 4;                      // appended rows per call
 constexpr int MERGE_FEW = 16;  // chunks of the one-lane-per-dim merge
-constexpr int MERGE_J = 9;  // chunks per merge lane: 16 lanes x 9 >= the at most 124 splits of a decode plan
+constexpr int MERGE_JMAX = 16;  // chunks per merge lane: 16 lanes x 16 >= the at most 248 splits of a decode plan
 
 // One stage of this wave's registers: K operands (16 keys x 128 dims) and V operands (64 keys x 32 dims).
 struct StageRegs {
@@ -348,6 +348,7 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
 // Merge of the split-K partials: work-group (token, head, quarter of the dims); its 256 threads are 16 chunk lanes x
 // 16 dim lanes (4 dims each), so every chunk's 64 dims are one coalesced 256-byte read and all chunks are in flight at
 // once; the 16 chunk lanes are then summed in LDS.
+template <int MERGE_J>  // chunks per chunk lane: 9 for up to 144 splits, 16 for up to 256 (fewer loads when few)
 __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ part, int rpk, int n, int start,
                                                       int span, int nch, const float* __restrict__ gate,
                                                       float* __restrict__ out) {
@@ -486,7 +487,7 @@ DecodePlan decode_plan(int n, int ntok, int start) {
 hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float* q, int ntok, int n, int start,
                               float scale, const DecodePlan& p, const DecodeWs& ws, const FusedAppend& fa,
                               const Launch& L) {
-    if (p.nch > ws.max_chunks || p.nch - p.c0 > 16 * MERGE_J) return hipErrorInvalidValue;
+    if (p.nch > ws.max_chunks || p.nch - p.c0 > 16 * MERGE_JMAX) return hipErrorInvalidValue;
     char* b = (char*)base;
     void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
     void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
@@ -498,11 +499,15 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
 
 hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,
                         float* out, const Launch& L) {
-    if (nch > 16 * MERGE_J) return hipErrorInvalidValue;
+    if (nch > 16 * MERGE_JMAX) return hipErrorInvalidValue;
     if (nch <= MERGE_FEW)
         return launch(merge_few, dim3((ntok * QH + 3) / 4), dim3(256), L, part, rpk, ntok, n, start, span, nch, gate,
                       out);
-    return launch(decode_combine, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, span, nch, gate, out);
+    if (nch <= 16 * 9)
+        return launch(decode_combine<9>, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, span, nch, gate,
+                      out);
+    return launch(decode_combine<MERGE_JMAX>, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, span, nch,
+                  gate, out);
 }
 
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,

@@ -153,7 +153,7 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
         (void)hipGetLastError();
         return fail(MKV_E_NOMEM, "mkv_create: hipMalloc of %zu bytes failed", bytes);
     }
-    h->dws.max_chunks = std::min(ctx / 64 + 2, 128);  // decode splits: one per 64-position stage, at most 124
+    h->dws.max_chunks = std::min(ctx / 64 + 2, 256);  // decode splits: f16 one per 64-position stage, at most 124; f32 at most 248
     size_t dws_bytes = (size_t)KVH * ROWS * h->dws.max_chunks * PART * sizeof(float);
     e = hipMalloc(&h->dws.part, dws_bytes);
     if (e != hipSuccess) {
