@@ -1,0 +1,63 @@
+"""The path under HIP graph capture. The reference records its commands once and replays them every step
+(engine.rs:571-597; only uniforms change); the MI355X equivalent is a captured graph. A verify step
+(mkv_append_decode: fused append + decode + merge) and a prefill are captured through the C ABI on torch's capture
+stream and replayed several times, with eager work of the same store in between; every replay must equal the eager
+call of the same step bit for bit (a captured step re-appends its rows at the same positions, so replays are
+idempotent). The calls make no allocation, host synchronization or memset once the store exists (the prefill
+workspace is grown by one eager call before capture).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import kv_inputs, q_inputs
+
+pytestmark = pytest.mark.gpu
+
+F16, F32 = 0, 1
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("fmt", [F16, F32])
+def test_captured_verify_and_prefill_replay_bit_identical(torch_gpu, fmt):
+    import mechta_amd as mk
+    torch = torch_gpu
+    print(f"graph capture fmt={fmt}", flush=True)
+    n0, ntok, T = 3000, 4, 64
+    kn, v = kv_inputs(71, n0 + T)
+    tab = O.rope_tables(0, n0 + T)
+    q4, q64 = _dev(torch, q_inputs(72, ntok)), _dev(torch, q_inputs(73, T))
+    with mk.KvStore(1, 8192, fmt) as st:
+        for p in range(0, n0 - 1, 512):
+            m = min(512, n0 - 1 - p)
+            st.append(0, p, _dev(torch, kn[p:p + m]), _dev(torch, v[p:p + m]), _dev(torch, tab[p:p + m]))
+        step_in = [_dev(torch, a[n0 - 1:n0 - 1 + ntok]) for a in (kn, v, tab)]
+        out_e = st.append_decode(0, n0, *step_in, q4).clone()
+        pf_e = st.prefill(0, q64, n0 + ntok - T).clone()  # the last T positions as a prefill block (grows ws)
+        st.set_len(n0 - 1)
+        torch.cuda.synchronize()
+
+        out_g = torch.empty_like(out_e)
+        pf_g = torch.empty_like(pf_e)
+        g = torch.cuda.CUDAGraph()
+        base_stream = torch.cuda.current_stream()
+        with torch.cuda.graph(g):
+            st.set_stream(torch.cuda.current_stream())
+            st.append_decode(0, n0, *step_in, q4, out=out_g)
+            st.prefill(0, q64, n0 + ntok - T, out=pf_g)
+        st.set_stream(base_stream)
+        torch.cuda.synchronize()
+        for r in range(4):
+            out_g.fill_(float("nan"))
+            pf_g.fill_(float("nan"))
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out_g, out_e), f"replay {r}: verify output differs from the eager call"
+            assert torch.equal(pf_g, pf_e), f"replay {r}: prefill output differs from the eager call"
+            # eager work of the same store between replays: a decode at another length
+            other = st.decode(0, q4, n0 - 500)
+            torch.cuda.synchronize()
+            assert torch.isfinite(other).all()
