@@ -186,10 +186,13 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             for (int i = 1; i < 16; i++) mt = fmaxf(mt, Scur[b][i]);
             mt = xor32_op(mt, [](float a, float b) { return fmaxf(a, b); });
             mt *= scale2;  // scale2 > 0: the max of the scaled scores is the scaled max
-            float mr = m[b];
-            if (m[b] == NEG_INF || mt > m[b] + LAZY2) mr = fmaxf(m[b], mt);
-            const float cf = (m[b] == NEG_INF) ? 1.f : fast_exp2(m[b] - mr);
-            if (__any(cf != 1.f)) {
+            // the reference max moves when first or when the tile max exceeds it by more than 8; O and the sum are
+            // rescaled only when a finite reference moved (rare: the exponential is not evaluated otherwise)
+            const bool rescale = m[b] != NEG_INF && mt > m[b] + LAZY2;
+            const float mr = m[b] == NEG_INF || rescale ? fmaxf(m[b], mt) : m[b];
+            float cf = 1.f;
+            if (__any(rescale)) {
+                cf = rescale ? fast_exp2(m[b] - mr) : 1.f;
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const float f = __shfl(cf, 8 * (i >> 2) + 4 * h + (i & 3));
