@@ -185,11 +185,11 @@ __global__ void __launch_bounds__(256 * NWG, 2) attn_f32(const float* __restrict
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         const float mn = fmaxf(m_run, mt);
         const float base = mn == NEG_INF ? 0.f : mn;
-        const float cf = m_run == NEG_INF ? 0.f : exp2f(m_run - mn);
+        const float cf = m_run == NEG_INF ? 0.f : fast_exp2(m_run - mn);
         float ls = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            sv[i] = exp2f(sv[i] - base);
+            sv[i] = fast_exp2(sv[i] - base);
             ls += sv[i];
         }
         ls += __shfl_xor(ls, 32);
