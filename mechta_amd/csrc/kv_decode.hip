@@ -44,6 +44,10 @@ struct StageRegs {
 
 // Stage operands in four register sets: K two stages ahead and V one stage ahead, two sets each (three or four
 // sets of whole stages, two or three stages in flight, measured slower).
+// EXACT = false: the reference's attn_dmx arithmetic (Q and P rounded to f16, f32 sums), for its 2- and 4-token
+// steps. EXACT = true: attn_fd's f32-class arithmetic, for one token and for windows (start > 0): Q and P are split
+// into f16 hi + lo and each product with the (exact f16) K or V takes two MFMA passes; the row sums add the f32 P.
+template <bool EXACT>
 __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane, _Float16* __restrict__ vplane,
                                                   size_t plane_elems, const float* __restrict__ q, int ntok, int n,
                                                   int start, float scale2, int s0, int nu,
@@ -75,6 +79,8 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     __shared__ __attribute__((aligned(16))) _Float16 ps[2][ROWS][PS_STRIDE];
     __shared__ __attribute__((aligned(16))) float cfs[2][ROWS];
     __shared__ __attribute__((aligned(16))) _Float16 qs[ROWS][QS_STRIDE];
+    __shared__ __attribute__((aligned(16))) _Float16 qsl[EXACT ? ROWS : 1][QS_STRIDE];      // EXACT: Q's lo part
+    __shared__ __attribute__((aligned(16))) _Float16 psl[EXACT ? 2 : 1][ROWS][PS_STRIDE];  // EXACT: P's lo part
     // fused append: the new rows' inputs (K normed, V, RoPE table) and their f16 store values
     __shared__ __attribute__((aligned(16))) float ain[2 * NEWMAX * HD + NEWMAX * 64];
     __shared__ __attribute__((aligned(16))) _Float16 newk[NEWMAX][HD];
@@ -165,8 +171,15 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
         const int idx = tid + 512 * i, row = idx >> 5, d8 = (idx & 31) * 8, tq = row >> 3;
         float4 x0 = xq[i][0], x1 = xq[i][1];
         if (tq >= ntok) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
-        *(half8*)&qs[row][d8] = half8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
-                                      (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
+        if constexpr (EXACT) {
+            half8 hi, lo;
+            split8(f32x4{x0.x, x0.y, x0.z, x0.w}, f32x4{x1.x, x1.y, x1.z, x1.w}, hi, lo);
+            *(half8*)&qs[row][d8] = hi;
+            *(half8*)&qsl[row][d8] = lo;
+        } else {
+            *(half8*)&qs[row][d8] = half8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
+                                          (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
+        }
     }
     lds_barrier();
 
@@ -195,6 +208,10 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
             const half8 q1 = *(const half8*)&qs[16 + l16][128 * dh + 32 * s + 8 * g4];
             s4[0] = mfma16(kk[s], q0, s4[0]);
             s4[1] = mfma16(kk[s], q1, s4[1]);
+            if constexpr (EXACT) {
+                s4[0] = mfma16(kk[s], *(const half8*)&qsl[l16][128 * dh + 32 * s + 8 * g4], s4[0]);
+                s4[1] = mfma16(kk[s], *(const half8*)&qsl[16 + l16][128 * dh + 32 * s + 8 * g4], s4[1]);
+            }
         }
         return [&, s4, buf]() {
 #pragma unroll
@@ -224,13 +241,25 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
         if (m_run == NEG_INF || mt > m_run + LAZY2) mr = fmaxf(m_run, mt);
         const float cf = m_run == NEG_INF ? 1.f : fast_exp2(m_run - mr);
         const float base = mr == NEG_INF ? 0.f : mr;  // masked scores are -inf: 2^-inf = 0
-        typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-        const half2v p01 = {(_Float16)fast_exp2(sv[0] - base), (_Float16)fast_exp2(sv[1] - base)};
-        const half2v p23 = {(_Float16)fast_exp2(sv[2] - base), (_Float16)fast_exp2(sv[3] - base)};
-        const half2v one2 = {(_Float16)1.f, (_Float16)1.f};
-        // l adds the f16-rounded P, summed in f32 (v_dot2_f32_f16 is exact for these products by 1)
-        float psum = __builtin_amdgcn_fdot2(p23, one2, __builtin_amdgcn_fdot2(p01, one2, 0.f, false), false);
-        *(uint2*)&ps[buf][srow][4 * sq] = uint2{__builtin_bit_cast(unsigned, p01), __builtin_bit_cast(unsigned, p23)};
+        float psum;
+        if constexpr (EXACT) {  // f32 P: its hi and lo f16 parts for the matrix units, the f32 values for the sum
+            const f32x4 pf = {fast_exp2(sv[0] - base), fast_exp2(sv[1] - base), fast_exp2(sv[2] - base),
+                              fast_exp2(sv[3] - base)};
+            psum = (pf.x + pf.y) + (pf.z + pf.w);
+            half4 hi, lo;
+            split4(pf, hi, lo);
+            *(half4*)&ps[buf][srow][4 * sq] = hi;
+            *(half4*)&psl[buf][srow][4 * sq] = lo;
+        } else {
+            typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+            const half2v p01 = {(_Float16)fast_exp2(sv[0] - base), (_Float16)fast_exp2(sv[1] - base)};
+            const half2v p23 = {(_Float16)fast_exp2(sv[2] - base), (_Float16)fast_exp2(sv[3] - base)};
+            const half2v one2 = {(_Float16)1.f, (_Float16)1.f};
+            // l adds the f16-rounded P, summed in f32 (v_dot2_f32_f16 is exact for these products by 1)
+            psum = __builtin_amdgcn_fdot2(p23, one2, __builtin_amdgcn_fdot2(p01, one2, 0.f, false), false);
+            *(uint2*)&ps[buf][srow][4 * sq] =
+                uint2{__builtin_bit_cast(unsigned, p01), __builtin_bit_cast(unsigned, p23)};
+        }
         psum = reduce16(psum, [](float a, float b) { return a + b; });
         l_run = l_run * cf + psum;
         m_run = mr;
@@ -277,7 +306,10 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
                     if (k0 + 16 * s2 + 8 * h + jj >= kend) vb[s2][jj] = (_Float16)0.f;
         }
 #pragma unroll
-        for (int s2 = 0; s2 < KPS / 16; s2++) O = mfma32(pa[s2], vb[s2], O);
+        for (int s2 = 0; s2 < KPS / 16; s2++) {
+            O = mfma32(pa[s2], vb[s2], O);
+            if constexpr (EXACT) O = mfma32(*(const half8*)&psl[buf][r][16 * s2 + 8 * h], vb[s2], O);
+        }
     };
 
     // Software pipeline, one barrier per stage. Iteration j: issue the loads of K for stage j + 2 and of V for stage
@@ -493,7 +525,8 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
     void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
     const float scale2 = scale * LOG2E;
     if (g.fmt != 0) return hipErrorNotSupported;
-    return launch(decode_f16, dim3(p.nch, KVH), dim3(512), L, kp, vp, g.plane_elems, q, ntok, n, start, scale2,
+    return launch(ntok == 1 || start > 0 ? decode_f16<true> : decode_f16<false>, dim3(p.nch, KVH), dim3(512), L, kp, vp,
+                  g.plane_elems, q, ntok, n, start, scale2,
                   p.s0, p.nu, ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
 }
 

@@ -82,6 +82,7 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
     const _Float16* V = vplane + (size_t)kvh * plane_elems;
 
     __shared__ __attribute__((aligned(16))) unsigned char ring[NSLOT * SLOT_BYTES];
+    __shared__ __attribute__((aligned(16))) float cfs[NW][32];  // rescale factors of a wave's rows
     const int ntiles = (ce - cs + 32 * SUB - 1) / (32 * SUB);
     auto issue = [&](int j) {  // each wave copies 1/NW of tile j's K blocks and V groups into slot j % NSLOT
         constexpr int PART_BYTES = SUB * TILE_BYTES / NW;
@@ -184,7 +185,7 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             float mt = Scur[b][0];
 #pragma unroll
             for (int i = 1; i < 16; i++) mt = fmaxf(mt, Scur[b][i]);
-            mt = xor32_op(mt, [](float a, float b) { return fmaxf(a, b); });
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
             mt *= scale2;  // scale2 > 0: the max of the scaled scores is the scaled max
             // the reference max moves when first or when the tile max exceeds it by more than 8; O and the sum are
             // rescaled only when a finite reference moved (rare: the exponential is not evaluated otherwise)
@@ -192,12 +193,19 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             const float mr = m[b] == NEG_INF || rescale ? fmaxf(m[b], mt) : m[b];
             float cf = 1.f;
             if (__any(rescale)) {
+                // register i of O holds row 8(i/4) + 4h + i%4, whose factor lane (that row) holds: the 32 factors pass
+                // through this wave's LDS row (constant offsets, no per-register lane index to keep)
                 cf = rescale ? fast_exp2(m[b] - mr) : 1.f;
+                if (h == 0) cfs[w][r] = cf;
+                __builtin_amdgcn_wave_barrier();
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const float f = __shfl(cf, 8 * (i >> 2) + 4 * h + (i & 3));
+                for (int a = 0; a < 4; a++) {
+                    const f32x4 f = *(const f32x4*)&cfs[w][8 * a + 4 * h];
 #pragma unroll
-                    for (int nb = 0; nb < 8; nb++) O[b][nb][i] *= f;
+                    for (int nb = 0; nb < 8; nb++) {
+#pragma unroll
+                        for (int q = 0; q < 4; q++) O[b][nb][4 * a + q] *= f[q];
+                    }
                 }
             }
             m[b] = mr;

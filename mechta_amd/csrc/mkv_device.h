@@ -87,17 +87,6 @@ __device__ inline float reduce16(float x, Op op) {
     return x;
 }
 
-// Value of lane l ^ 32 (the other half of the wave) with v_permlane32_swap: a lane swap in the ALU, no LDS round trip.
-// After swapping the upper half of one copy with the lower half of another, the copies hold [x_lo, x_lo] and
-// [x_hi, x_hi]; lane l's own value is in one and its partner's in the other, so a symmetric op of the two is the
-// op of x_l and x_(l^32).
-template <typename Op>
-__device__ inline float xor32_op(float x, Op op) {
-    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
-                                                    false, false);
-    return op(__builtin_bit_cast(float, p[0]), __builtin_bit_cast(float, p[1]));
-}
-
 // Raw buffer access: a 16-byte load whose offset lies past the resource's `bytes` returns zeros without a memory
 // access, which masks lanes or whole loads without a branch (and so without the waits a branch around a load makes
 // the compiler insert).
