@@ -72,3 +72,38 @@ def test_prefill_max_jump(torch_gpu, fmt):
                           what="f32 prefill, max jump")
     else:
         assert_attn_close(out[sel], O.attn_fa_mx(kc, vc, q, n0, sel=sel), what="f16 prefill, max jump")
+
+
+@pytest.mark.parametrize("fmt", [F16, F32])
+@pytest.mark.parametrize("sliding", [False, True])
+def test_flint_max_jump(torch_gpu, fmt, sliding):
+    """The Flint kernels (exact running max, sinks) with keys boosted 24x: one-token decode and a 64-token block."""
+    from mechta_amd import flint as mf
+    torch = torch_gpu
+    print(f"rescale flint fmt={fmt} sliding={sliding}", flush=True)
+    H, KVH, D = 32, 4, 128
+    npos = 2600
+    r = np.random.default_rng(95)
+    k = r.standard_normal((npos, KVH, D), dtype=np.float32)
+    v = r.standard_normal((npos, KVH, D), dtype=np.float32)
+    for b in (700, 2200, 2400, npos - 1):
+        k[b] *= 24.0
+    sinks = r.standard_normal(H, dtype=np.float32)
+    win = 513 if sliding else 0
+    with mf.FlintStore(1, 4096, fmt, sliding=[sliding]) as st:
+        rows = st.rows(0)
+        kc, vc = O.fl_new_cache(rows, fmt), O.fl_new_cache(rows, fmt)
+        for p in range(0, npos - 64, 512):
+            m = min(512, npos - 64 - p)
+            st.append(0, p, _dev(torch, k[p:p + m]), _dev(torch, v[p:p + m]))
+            O.fl_kv_write(fmt, kc, vc, p, k[p:p + m], v[p:p + m])
+        p0 = npos - 64
+        st.append(0, p0, _dev(torch, k[p0:]), _dev(torch, v[p0:]))
+        O.fl_kv_write(fmt, kc, vc, p0, k[p0:], v[p0:])
+        q = r.standard_normal((64, H, D), dtype=np.float32)
+        blk = st.attend(0, p0, _dev(torch, q), _dev(torch, sinks)).cpu().numpy()
+        one = st.attend(0, npos - 1, _dev(torch, q[-1:]), _dev(torch, sinks)).cpu().numpy()
+    tol = dict(atol=1e-4, rtol=1e-5)
+    assert_attn_close(blk, O.fl_attn_pf(fmt, kc, vc, q, p0, win, sinks), what="flint block, max jump", **tol)
+    assert_attn_close(one[0], O.fl_attn_fd(fmt, kc, vc, q[-1], npos - 1, win, sinks), what="flint one token, max jump",
+                      **tol)
