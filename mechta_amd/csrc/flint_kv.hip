@@ -259,6 +259,231 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
     }
 }
 
+// Prefill of an f16 cache: work-group = (32 tokens of the block, key split, kv head), 8 waves of 4 tokens x 8 heads
+// = 32 query rows each. The split's 32-key tiles (8 KB of K, 8 KB of V, contiguous: a tile is one 32-row block of
+// the ring) stream through an LDS ring filled by direct global->LDS loads and shared by the 8 waves, so a key is
+// fetched once per 32 tokens, not once per 4. Per tile and wave:
+//   S^T[32 keys][32 rows] = K . Q^T   8 dim steps x 2 v_mfma_f32_32x32x16_f16 (A = K rows in key_perm order from
+//                                     LDS, exact in f16; B = Q split hi + lo, in registers for the whole split)
+//   online softmax in registers with a lazy reference max (moves when first or when the tile maximum exceeds it by
+//   more than 8; the partial's m is that reference, which the merge treats like any other), f32 P
+//   O[32 rows][128] += P . V          2 key steps x 4 dim blocks x 2 (A = P split hi + lo from the S registers,
+//                                     B = V from LDS, exact)
+// The result is the same f32-class arithmetic as fl_attn; only the summation order differs.
+#ifndef FL_PF_SUB
+#define FL_PF_SUB 2
+#endif
+#ifndef FL_PF_NSLOT
+#define FL_PF_NSLOT 4
+#endif
+constexpr int PF_NW = 8;                                      // waves per work-group
+constexpr int PF_PT = 4 * PF_NW;                              // tokens per work-group
+constexpr int PF_SUB = FL_PF_SUB;                             // 32-key tiles per ring slot (per barrier)
+constexpr int PF_NSLOT = FL_PF_NSLOT;                         // ring slots: PF_NSLOT - 1 in flight
+constexpr int PF_TILE = TILE * HD * 2;                        // K (or V) bytes of one f16 tile
+constexpr int PF_SLOT = 2 * PF_SUB * PF_TILE;                 // K tiles, then V tiles of a slot
+constexpr int PF_LPT = 2 * PF_SUB * PF_TILE / PF_NW / 1024;   // direct loads per wave and slot
+static_assert(PF_TILE / PF_NW == 1024, "one direct load per wave and tile");
+static_assert((PF_NSLOT - 2) * PF_LPT <= 63, "vmcnt range");
+
+template <int N>
+__device__ inline void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+template <int L>  // wait until at most `later` slots (PF_LPT direct loads each) of this wave are pending
+__device__ inline void pf_wait(int later) {
+    if constexpr (L == 0) {
+        vm_wait<0>();
+    } else {
+        if (later >= L) vm_wait<L * PF_LPT>();
+        else pf_wait<L - 1>(later);
+    }
+}
+
+__global__ void __launch_bounds__(PF_NW * 64) fl_pf16(const _Float16* __restrict__ kplane,
+                                                      const _Float16* __restrict__ vplane, size_t plane_elems,
+                                                      int rows, const float* __restrict__ q, int T, int pos0, int win,
+                                                      float scale2, int klo, int span, int nch,
+                                                      float* __restrict__ part) {
+    // XCD-aware order (as the decode and prefill kernels): the token blocks of one (split, kv head) on one XCD
+    const int G = gridDim.x, Lb = blockIdx.x;
+    const int W = G % NXCD == 0 ? (Lb % NXCD) * (G / NXCD) + Lb / NXCD : Lb;
+    const int nblk = (T + PF_PT - 1) / PF_PT;
+    const int rb = W % nblk, c = (W / nblk) % nch, kvh = W / nblk / nch;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, r = lane & 31;
+    const int tb = rb * PF_PT, tlast = min(T - 1, tb + PF_PT - 1);
+    const int lo_first = window_lo(pos0 + tb, win);  // the block's earliest visible position
+    const int kend = pos0 + tlast + 1;               // keys [lo_first, kend) hold the block's positions
+    const int cs = klo + chunk_lo(c, span, nch), ce = c + 1 < nch ? klo + chunk_lo(c + 1, span, nch) : klo + span;
+    const int lo = max(cs, lo_first / TILE * TILE), hi = min(ce, kend);  // keys of this split, lo a tile start
+    const int nt32 = hi > lo ? (hi - lo + TILE - 1) / TILE : 0;
+    const int ntiles = (nt32 + PF_SUB - 1) / PF_SUB;  // ring slots to stream
+    const _Float16* K = kplane + (size_t)kvh * plane_elems;
+    const _Float16* V = vplane + (size_t)kvh * plane_elems;
+
+    __shared__ __attribute__((aligned(16))) unsigned char ring[PF_NSLOT * PF_SLOT];
+    __shared__ __attribute__((aligned(16))) float cfs[PF_NW][32];  // rescale factors of a wave's rows
+    auto issue = [&](int j) {  // each wave copies 1 KB of every K and V tile of slot j
+        unsigned char* dst = ring + (j % PF_NSLOT) * PF_SLOT + w * 1024;
+#pragma unroll
+        for (int u = 0; u < PF_SUB; u++) {
+            // a 32-position tile is one 32-row block of the ring (rows are a multiple of 32), K and V alike; tiles
+            // past the split's end stay inside the plane and are never computed
+            const size_t off = (size_t)((lo + TILE * (PF_SUB * j + u)) % rows) * HD;
+            dma16((const unsigned char*)(K + off) + w * 1024 + lane * 16, dst + u * PF_TILE);
+            dma16((const unsigned char*)(V + off) + w * 1024 + lane * 16, dst + (PF_SUB + u) * PF_TILE);
+        }
+    };
+    for (int j = 0; j < PF_NSLOT - 1 && j < ntiles; j++) issue(j);
+
+    // Q as the B operand of S^T: lane (r, h) holds row r (token tr, head r % 8), dims 16s + 8h .. +7 of step s, split
+    // into f16 hi + lo; rows of tokens past the block are zero and see no key
+    const int tr = tb + 4 * w + (r >> 3);
+    const int vlo = tr < T ? window_lo(pos0 + tr, win) : 0, vhi = tr < T ? pos0 + tr + 1 : 0;  // row sees [vlo, vhi)
+    half8 qh[8], ql[8];
+    {
+        const float* qrow = q + ((size_t)min(tr, T - 1) * QH + kvh * GQA + (r & 7)) * HD + 8 * h;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            f32x4 x0 = *(const f32x4*)(qrow + 16 * s), x1 = *(const f32x4*)(qrow + 16 * s + 4);
+            if (tr >= T) x0 = x1 = f32x4{};
+            split8(x0, x1, qh[s], ql[s]);
+        }
+    }
+    const int kaddr = h * 512 + key_perm(r) * 16;
+    float m = NEG_INF, lsum = 0.f;
+    f32x16 O[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) O[nb] = f32x16{};
+
+    // V rows of a slot outside [lo_first, kend) may be other positions' or never written: zero them in LDS so that
+    // 0 * V stays finite (K there only meets masked scores)
+    auto zero_v = [&](int j) {
+        unsigned short* Vz = (unsigned short*)(ring + (j % PF_NSLOT) * PF_SLOT + PF_SUB * PF_TILE);
+        const int k0 = lo + TILE * PF_SUB * j;
+        for (int i = tid; i < PF_SUB * TILE * HD; i += PF_NW * 64) {
+            const int key = k0 + (i / (8 * HD)) * 8 + (i & 7);  // group i / 1024, position i % 8 in the group
+            if (key < lo_first || key >= kend) Vz[i] = 0;
+        }
+    };
+    for (int j = 0; j < ntiles; j++) {
+        pf_wait<PF_NSLOT - 2>(min(ntiles - 1 - j, PF_NSLOT - 2));
+        lds_barrier();  // slot j is in LDS for every wave; every wave is done with slot j - 1
+        if (j + PF_NSLOT - 1 < ntiles) issue(j + PF_NSLOT - 1);  // into the slot of j - 1
+        const int ks0 = lo + TILE * PF_SUB * j;
+        if (ks0 < lo_first || ks0 + TILE * PF_SUB > kend) {
+            zero_v(j);
+            lds_barrier();
+        }
+#pragma unroll
+        for (int u = 0; u < PF_SUB; u++) {
+            const int k0 = ks0 + TILE * u;
+            if (k0 >= hi) break;
+            const unsigned char* Ks = ring + (j % PF_NSLOT) * PF_SLOT + u * PF_TILE;
+            const unsigned char* Vs = ring + (j % PF_NSLOT) * PF_SLOT + (PF_SUB + u) * PF_TILE;
+            // two independent chains (hi and lo of Q), added once: back-to-back MFMAs never wait on each other
+            f32x16 Sh = f32x16{}, Sl = f32x16{};
+            constexpr int KP = 3;  // K operands in flight ahead of the MFMAs
+            half8 kbuf[KP];
+#pragma unroll
+            for (int s = 0; s < KP; s++) kbuf[s] = *(const half8*)(Ks + kaddr + s * 1024);
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const half8 ka = kbuf[s % KP];
+                if (s + KP < 8) kbuf[s % KP] = *(const half8*)(Ks + kaddr + (s + KP) * 1024);
+                Sh = mfma32(ka, qh[s], Sh);
+                Sl = mfma32(ka, ql[s], Sl);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, KP, 0);
+#pragma unroll
+            for (int s = 0; s < 8 - KP; s++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * KP, 0);
+            f32x16 S = Sh + Sl;
+            // register i of lane (r, h) is key 8h + i (i < 8) or 16 + 8h + i - 8 of the tile for row r
+            if (!__all(k0 >= vlo && k0 + TILE <= vhi)) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int key = k0 + 8 * h + i + (i >= 8 ? 8 : 0);
+                    S[i] = (key >= vlo && key < vhi) ? S[i] : NEG_INF;
+                }
+            }
+            float mt = S[0];
+#pragma unroll
+            for (int i = 1; i < 16; i++) mt = fmaxf(mt, S[i]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            mt *= scale2;  // scale2 > 0: the max of the scaled scores is the scaled max
+            const bool rescale = m != NEG_INF && mt > m + LAZY2;
+            const float mr = m == NEG_INF || rescale ? fmaxf(m, mt) : m;
+            float cf = 1.f;
+            if (__any(rescale)) {
+                // register i of O holds row 8(i/4) + 4h + i%4, whose factor lane (that row) holds: the 32 factors
+                // pass through this wave's LDS row
+                cf = rescale ? fast_exp2(m - mr) : 1.f;
+                if (h == 0) cfs[w][r] = cf;
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int a = 0; a < 4; a++) {
+                    const f32x4 f = *(const f32x4*)&cfs[w][8 * a + 4 * h];
+#pragma unroll
+                    for (int nb = 0; nb < 4; nb++) {
+#pragma unroll
+                        for (int qq = 0; qq < 4; qq++) O[nb][4 * a + qq] *= f[qq];
+                    }
+                }
+            }
+            m = mr;
+            const float base = mr == NEG_INF ? 0.f : mr;
+            float p[16], ls = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                p[i] = fast_exp2(__builtin_fmaf(S[i], scale2, -base));
+                ls += p[i];
+            }
+            lsum = lsum * cf + ls;
+            half8 ph[2], pl[2];
+#pragma unroll
+            for (int k = 0; k < 2; k++)
+                split8(f32x4{p[8 * k], p[8 * k + 1], p[8 * k + 2], p[8 * k + 3]},
+                       f32x4{p[8 * k + 4], p[8 * k + 5], p[8 * k + 6], p[8 * k + 7]}, ph[k], pl[k]);
+            // key step k: keys 16k + 8h .. +7 = V group 2k + h; dim block nb: dims 32nb + r
+            half8 vb[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                vb[i] = *(const half8*)(Vs + (2 * (i >> 2) + h) * (HD * 16) + (32 * (i & 3) + r) * 16);
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++) O[nb] = mfma32(ph[k], vb[4 * k + nb], O[nb]);
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++) O[nb] = mfma32(pl[k], vb[4 * k + nb], O[nb]);
+            }
+        }
+    }
+
+    // partials [kvh][row < 8T][split][PART] of this wave's rows of present tokens (empty splits included: m = -inf,
+    // l = 0, acc = 0, which the merge weighs 0)
+    lsum += __shfl_xor(lsum, 32);
+    const int t0 = tb + 4 * w;
+    const size_t rbase = (size_t)kvh * T * GQA + (size_t)t0 * GQA;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int ri = 8 * (i >> 2) + 4 * h + (i & 3);
+        if (t0 + (ri >> 3) < T) {
+            float* pp = part + ((rbase + ri) * nch + c) * PART + PACC + r;
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++) pp[32 * nb] = O[nb][i];
+        }
+    }
+    if (h == 0 && t0 + (r >> 3) < T) {
+        float* pp = part + ((rbase + r) * nch + c) * PART;
+        pp[0] = m;
+        pp[1] = lsum;
+    }
+}
+
 // Merge of the splits with the sink (attn_fd_merge, flint_attn.wgsl:241-257): M = max(sink, m_c), out =
 // sum_c 2^(m_c - M) acc_c / (2^(sink - M) + sum_c 2^(m_c - M) l_c), all in log2 units. Work-group = row (token, head);
 // its 256 threads are 8 split lanes x 32 dim lanes (4 dims each): every split of the row is loaded in one round trip
@@ -633,10 +858,10 @@ __global__ void __launch_bounds__(256) fl_merge_few(const float* __restrict__ pa
 
 }  // namespace
 
-Plan plan(int pos0, int T, int win) {
+Plan plan(int fmt, int pos0, int T, int win) {
     const int lo0 = win > 0 && pos0 + 1 > win ? pos0 + 1 - win : 0;
     const int klo = lo0 / 32 * 32, span = pos0 + T - klo;
-    const int nrb = (T + 3) / 4;
+    int nrb = (T + 3) / 4;
     int nch;
     if (T <= 2) {  // fl_dec16
         nch = span / FL_DEC_SPLIT;
@@ -644,6 +869,12 @@ Plan plan(int pos0, int T, int win) {
     } else if (T <= 4) {  // one block of fl_attn: splits of at least 128 positions, 64 per kv head at most
         nch = span / 128;
         nch = nch > 64 ? 64 : nch;
+    } else if (fmt == 0) {  // fl_pf16: blocks of 32 tokens, about one work-group per CU, splits of 64 positions or more
+        nrb = (T + PF_PT - 1) / PF_PT;
+        nch = 256 / (nrb * KVH);
+        const int most = span / 64, room = WS_ROWS / (T * GQA);
+        nch = nch > most ? most : nch;
+        nch = nch > room ? room : nch > 16 ? 16 : nch;
     } else {
         nch = 512 / (nrb * KVH);
         const int most = span / 128;
@@ -653,11 +884,11 @@ Plan plan(int pos0, int T, int win) {
     return Plan{klo, span, nch, nrb};
 }
 
-size_t ws_floats() { return (size_t)KVH * 4096 * PART; }
+size_t ws_floats() { return (size_t)KVH * WS_ROWS * PART; }
 
 hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const float* q, int T, int pos0, int win,
                        const Plan& p, float* ws, const float* sinks, float* out, hipStream_t st) {
-    if ((size_t)T * GQA * p.nch > 4096) return hipErrorInvalidValue;  // the workspace's rows x splits per kv head
+    if ((size_t)T * GQA * p.nch > WS_ROWS) return hipErrorInvalidValue;  // the workspace's rows x splits per kv head
     const size_t pe = (size_t)rows * HD;
     const float scale2 = (1.0f / 11.313708498984761f) * LOG2E;  // 1/sqrt(128) (flint_attn.wgsl:92, 189) in log2 units
     const dim3 grid(p.nrb * p.nch * KVH);
@@ -673,11 +904,12 @@ hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const 
                             p.span, p.nch, p.nrb, ws)
                    : launch(fl_attn<1, 2, 2>, grid, dim3(512), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
                             p.span, p.nch, p.nrb, ws);
-    else
-        e = T <= 4 ? launch(fl_attn<0, 1, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
-                            p.span, p.nch, p.nrb, ws)
-                   : launch(fl_attn<0, 2, 2>, grid, dim3(512), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
-                            p.span, p.nch, p.nrb, ws);
+    else if (T <= 4)
+        e = launch(fl_attn<0, 1, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo, p.span,
+                   p.nch, p.nrb, ws);
+    else  // f16 prefill: 32-token blocks over an LDS ring
+        e = launch(fl_pf16, grid, dim3(PF_NW * 64), L, (const _Float16*)kp, (const _Float16*)vp, pe, rows, q, T, pos0,
+                   win, scale2, p.klo, p.span, p.nch, ws);
     if (e != hipSuccess) return e;
     if (p.nch > 8 * MERGE_J) return hipErrorInvalidValue;
     if (p.nch <= MERGE_FEW)
