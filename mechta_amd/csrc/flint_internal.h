@@ -28,12 +28,12 @@ __host__ __device__ inline size_t v_off16(int r, int d) {
 }
 
 // Splits of one attention call: keys [klo, klo + span) (klo = the first token's window start rounded down to 32),
-// nch splits at chunk_lo boundaries, nrb token blocks (4 tokens; 32 for the prefill of an f16 cache).
+// nch splits at chunk_lo boundaries, nrb token blocks (4 tokens; 32 for a prefill of more than 4).
 struct Plan {
     int klo, span, nch, nrb;
 };
 constexpr int WS_ROWS = 16384;  // rows x splits per kv head that the split partials hold
-Plan plan(int fmt, int pos0, int T, int win);
+Plan plan(int pos0, int T, int win);
 size_t ws_floats();  // split partials of any plan: 4 kv heads x WS_ROWS x PART
 
 hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const float* q, int T, int pos0, int win,

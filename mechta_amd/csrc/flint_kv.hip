@@ -1,8 +1,9 @@
 // flint_kv.hip -- the Flint model's KV path: ring append, NEOX RoPE, conversion to the reference's row layout, and
 // sliding-window attention with per-head sinks (flint_attn.wgsl:1-257), for one decode token or a prefill block.
 //
-// Attention work-group: (block of 4 tokens, key split, kv head) = 32 query rows (token * 8 + head) against the split's
-// keys in tiles of 32 positions. The arithmetic is f32, as the reference's, taken on the f16 matrix units: f32
+// Three attention kernels: fl_dec16 (1-2 tokens, 16 query rows), fl_attn (3-4 tokens) and fl_pf (prefill blocks of
+// 5-512 tokens, 32 tokens per work-group sharing an LDS ring of K/V tiles). fl_attn's work-group: (block of 4 tokens,
+// key split, kv head) = 32 query rows (token * 8 + head) against the split's keys in tiles of 32 positions. The arithmetic is f32, as the reference's, taken on the f16 matrix units: f32
 // operands are split into f16 hi + lo and each product is three v_mfma_f32_32x32x16_f16 passes (hi.hi + hi.lo +
 // lo.hi, f32 accumulation), two where one side is an f16 cache's K or V (exact in f16). Per tile, wave w of a group
 // of 4:
@@ -54,8 +55,8 @@ struct TileRegs<0> {  // f16: K dims 32w + 16a + 8s .. +7 (a < 2); V keys 8q + 4
     half4 v[4];
 };
 
-template <int FMT, int NWG, int NBUF>  // NBUF: tiles in registers (NBUF - 1 in flight ahead of the one computed)
-__global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kplane, const void* __restrict__ vplane,
+template <int FMT, int NBUF>  // NBUF: tiles in registers (NBUF - 1 in flight ahead of the one computed)
+__global__ void __launch_bounds__(256) fl_attn(const void* __restrict__ kplane, const void* __restrict__ vplane,
                                                      size_t plane_elems, int rows, const float* __restrict__ q, int T,
                                                      int pos0, int win, float scale2, int klo, int span, int nch,
                                                      int nrb, float* __restrict__ part) {
@@ -64,7 +65,7 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
     const int G = gridDim.x, L = blockIdx.x;
     const int W = G % NXCD == 0 ? (L % NXCD) * (G / NXCD) + L / NXCD : L;
     const int rb = W % nrb, c = (W / nrb) % nch, kvh = W / nrb / nch;
-    const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 8, w = (tid >> 6) & 3, s = lane >> 5, r32 = lane & 31;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, s = lane >> 5, r32 = lane & 31;
     const int t0 = 4 * rb, nt = min(4, T - t0);
     const int lo_first = window_lo(pos0 + t0, win);  // the block's earliest visible position
     const int cs = klo + chunk_lo(c, span, nch), ce = c + 1 < nch ? klo + chunk_lo(c + 1, span, nch) : klo + span;
@@ -72,8 +73,8 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
     const int ntile = hi > lo ? (hi - lo + TILE - 1) / TILE : 0;
 
     __shared__ __attribute__((aligned(16))) _Float16 qh[32][QPAD], ql[32][QPAD];  // Q split: hi, lo
-    __shared__ f32x4 sx[2][NWG][4][4][64];  // partial S^T: [round parity][group][wave][register quad][lane]
-    for (int i = tid; i < 32 * HD / 8; i += 256 * NWG) {
+    __shared__ f32x4 sx[2][4][4][64];  // partial S^T: [tile parity][wave][register quad][lane]
+    for (int i = tid; i < 32 * HD / 8; i += 256) {
         const int row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
         f32x4 x0 = f32x4{}, x1 = f32x4{};
         if (t < T) {
@@ -137,8 +138,7 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
                 S = mfma2(X.k[a], bh, bl, S);
             }
         }
-        const int pb = (j / NWG) & 1;
-        f32x4(&sg)[4][4][64] = sx[pb][grp];
+        f32x4(&sg)[4][4][64] = sx[j & 1];
 #pragma unroll
         for (int a = 0; a < 4; a++) sg[w][a][lane] = f32x4{S[4 * a], S[4 * a + 1], S[4 * a + 2], S[4 * a + 3]};
         lds_barrier();
@@ -205,43 +205,17 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
 
     // a ring of NBUF register tiles: round r computes slot r % NBUF after issuing the loads of round r + NBUF - 1
     // into the slot round r - 1 freed (the slots are unrolled, so every index is a constant)
-    const int rounds = (ntile + NWG - 1) / NWG;
+    const int rounds = ntile;
     TileRegs<FMT> R[NBUF];
 #pragma unroll
-    for (int k = 0; k < NBUF - 1; k++) load(R[k], k * NWG + grp);
+    for (int k = 0; k < NBUF - 1; k++) load(R[k], k);
     for (int i0 = 0; i0 < rounds; i0 += NBUF) {
 #pragma unroll
         for (int k = 0; k < NBUF; k++) {
             if (i0 + k < rounds) {  // uniform in the work-group
-                load(R[(k + NBUF - 1) % NBUF], (i0 + k + NBUF - 1) * NWG + grp);
-                step(R[k], (i0 + k) * NWG + grp);
+                load(R[(k + NBUF - 1) % NBUF], i0 + k + NBUF - 1);
+                step(R[k], i0 + k);
             }
-        }
-    }
-
-    if constexpr (NWG == 2) {  // group 1's state into group 0 through LDS
-        __syncthreads();
-        float* ob = (float*)&sx[0][0][0][0][0];  // [wave][16][64], then m, l of 32 rows
-        float* ml = ob + 4 * 16 * 64;
-        if (grp == 1) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) ob[(w * 16 + i) * 64 + lane] = O[i];
-            if (w == 0 && s == 0) {
-                ml[r32] = m_run;
-                ml[32 + r32] = l_run;
-            }
-        }
-        __syncthreads();
-        if (grp == 1) return;
-        const float m1 = ml[r32], l1 = ml[32 + r32];
-        const float M = fmaxf(m_run, m1);
-        const float f0 = m_run == NEG_INF ? 0.f : exp2f(m_run - M), f1 = m1 == NEG_INF ? 0.f : exp2f(m1 - M);
-        l_run = l_run * f0 + l1 * f1;
-        m_run = M;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int row = 8 * (i >> 2) + 4 * s + (i & 3);
-            O[i] = O[i] * __shfl(f0, row) + ob[(w * 16 + i) * 64 + lane] * __shfl(f1, row);
         }
     }
 
@@ -259,52 +233,64 @@ __global__ void __launch_bounds__(256 * NWG) fl_attn(const void* __restrict__ kp
     }
 }
 
-// Prefill of an f16 cache: work-group = (32 tokens of the block, key split, kv head), 8 waves of 4 tokens x 8 heads
-// = 32 query rows each. The split's 32-key tiles (8 KB of K, 8 KB of V, contiguous: a tile is one 32-row block of
-// the ring) stream through an LDS ring filled by direct global->LDS loads and shared by the 8 waves, so a key is
-// fetched once per 32 tokens, not once per 4. Per tile and wave:
-//   S^T[32 keys][32 rows] = K . Q^T   8 dim steps x 2 v_mfma_f32_32x32x16_f16 (A = K rows in key_perm order from
-//                                     LDS, exact in f16; B = Q split hi + lo, in registers for the whole split)
+// Prefill: work-group = (32 tokens of the block, key split, kv head), 8 waves of 4 tokens x 8 heads = 32 query rows
+// each. The split's 32-key tiles (K and V of 32 positions, each contiguous: a tile is one 32-row block of the ring)
+// stream through an LDS ring filled by direct global->LDS loads and shared by the 8 waves, so a key is fetched once
+// per 32 tokens, not once per 4. Per tile and wave:
+//   S^T[32 keys][32 rows] = K . Q^T   8 dim steps of v_mfma_f32_32x32x16_f16 (A = K rows in key_perm order from
+//                                     LDS; B = Q split hi + lo, in registers for the whole split): 2 passes on an
+//                                     f16 cache (K exact), 3 on an f32 cache (K split as it leaves LDS)
 //   online softmax in registers with a lazy reference max (moves when first or when the tile maximum exceeds it by
 //   more than 8; the partial's m is that reference, which the merge treats like any other), f32 P
-//   O[32 rows][128] += P . V          2 key steps x 4 dim blocks x 2 (A = P split hi + lo from the S registers,
-//                                     B = V from LDS, exact)
+//   O[32 rows][128] += P . V          2 key steps x 4 dim blocks (A = P split hi + lo from the S registers, B = V
+//                                     from LDS): 2 passes (f16 V exact) or 3 (f32 V split)
 // The result is the same f32-class arithmetic as fl_attn; only the summation order differs.
-#ifndef FL_PF_SUB
-#define FL_PF_SUB 2
+#ifndef FL_PF_SUB16
+#define FL_PF_SUB16 2
+#endif
+#ifndef FL_PF_SUB32
+#define FL_PF_SUB32 1
 #endif
 #ifndef FL_PF_NSLOT
 #define FL_PF_NSLOT 4
 #endif
-constexpr int PF_NW = 8;                                      // waves per work-group
-constexpr int PF_PT = 4 * PF_NW;                              // tokens per work-group
-constexpr int PF_SUB = FL_PF_SUB;                             // 32-key tiles per ring slot (per barrier)
-constexpr int PF_NSLOT = FL_PF_NSLOT;                         // ring slots: PF_NSLOT - 1 in flight
-constexpr int PF_TILE = TILE * HD * 2;                        // K (or V) bytes of one f16 tile
-constexpr int PF_SLOT = 2 * PF_SUB * PF_TILE;                 // K tiles, then V tiles of a slot
-constexpr int PF_LPT = 2 * PF_SUB * PF_TILE / PF_NW / 1024;   // direct loads per wave and slot
-static_assert(PF_TILE / PF_NW == 1024, "one direct load per wave and tile");
-static_assert((PF_NSLOT - 2) * PF_LPT <= 63, "vmcnt range");
+constexpr int PF_NW = 8;               // waves per work-group
+constexpr int PF_PT = 4 * PF_NW;       // tokens per work-group
+constexpr int PF_NSLOT = FL_PF_NSLOT;  // ring slots: PF_NSLOT - 1 in flight
+
+template <int FMT>
+struct PfGeom {
+    static constexpr int BPE = FMT == 1 ? 4 : 2;
+    static constexpr int SUB = FMT == 1 ? FL_PF_SUB32 : FL_PF_SUB16;  // 32-key tiles per ring slot (per barrier)
+    static constexpr int TILE_BYTES = TILE * HD * BPE;                // K (or V) bytes of one tile
+    static constexpr int SLOT = 2 * SUB * TILE_BYTES;                 // K tiles, then V tiles of a slot
+    static constexpr int DPT = TILE_BYTES / PF_NW / 1024;             // direct loads per wave and K (or V) tile
+    static constexpr int LPT = 2 * SUB * DPT;                         // direct loads per wave and slot
+    static constexpr int EPG = 16 / BPE;                              // positions per V group
+    static_assert((PF_NSLOT - 2) * LPT <= 63, "vmcnt range");
+};
 
 template <int N>
 __device__ inline void vm_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-template <int L>  // wait until at most `later` slots (PF_LPT direct loads each) of this wave are pending
+template <int L, int LPT>  // wait until at most `later` slots (LPT direct loads each) of this wave are pending
 __device__ inline void pf_wait(int later) {
     if constexpr (L == 0) {
         vm_wait<0>();
     } else {
-        if (later >= L) vm_wait<L * PF_LPT>();
-        else pf_wait<L - 1>(later);
+        if (later >= L) vm_wait<L * LPT>();
+        else pf_wait<L - 1, LPT>(later);
     }
 }
 
-__global__ void __launch_bounds__(PF_NW * 64) fl_pf16(const _Float16* __restrict__ kplane,
-                                                      const _Float16* __restrict__ vplane, size_t plane_elems,
-                                                      int rows, const float* __restrict__ q, int T, int pos0, int win,
-                                                      float scale2, int klo, int span, int nch,
-                                                      float* __restrict__ part) {
+template <int FMT>
+__global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kplane, const void* __restrict__ vplane,
+                                                    size_t plane_elems, int rows, const float* __restrict__ q, int T,
+                                                    int pos0, int win, float scale2, int klo, int span, int nch,
+                                                    float* __restrict__ part) {
+    using Gm = PfGeom<FMT>;
+    constexpr int SUB = Gm::SUB, TB = Gm::TILE_BYTES, SLOT = Gm::SLOT;
     // XCD-aware order (as the decode and prefill kernels): the token blocks of one (split, kv head) on one XCD
     const int G = gridDim.x, Lb = blockIdx.x;
     const int W = G % NXCD == 0 ? (Lb % NXCD) * (G / NXCD) + Lb / NXCD : Lb;
@@ -317,21 +303,24 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf16(const _Float16* __restrict
     const int cs = klo + chunk_lo(c, span, nch), ce = c + 1 < nch ? klo + chunk_lo(c + 1, span, nch) : klo + span;
     const int lo = max(cs, lo_first / TILE * TILE), hi = min(ce, kend);  // keys of this split, lo a tile start
     const int nt32 = hi > lo ? (hi - lo + TILE - 1) / TILE : 0;
-    const int ntiles = (nt32 + PF_SUB - 1) / PF_SUB;  // ring slots to stream
-    const _Float16* K = kplane + (size_t)kvh * plane_elems;
-    const _Float16* V = vplane + (size_t)kvh * plane_elems;
+    const int ntiles = (nt32 + SUB - 1) / SUB;  // ring slots to stream
+    const unsigned char* K = (const unsigned char*)kplane + (size_t)kvh * plane_elems * Gm::BPE;
+    const unsigned char* V = (const unsigned char*)vplane + (size_t)kvh * plane_elems * Gm::BPE;
 
-    __shared__ __attribute__((aligned(16))) unsigned char ring[PF_NSLOT * PF_SLOT];
+    __shared__ __attribute__((aligned(16))) unsigned char ring[PF_NSLOT * SLOT];
     __shared__ __attribute__((aligned(16))) float cfs[PF_NW][32];  // rescale factors of a wave's rows
-    auto issue = [&](int j) {  // each wave copies 1 KB of every K and V tile of slot j
-        unsigned char* dst = ring + (j % PF_NSLOT) * PF_SLOT + w * 1024;
+    auto issue = [&](int j) {  // each wave copies 1/8 of every K and V tile of slot j
+        unsigned char* dst = ring + (j % PF_NSLOT) * SLOT + w * (TB / PF_NW);
 #pragma unroll
-        for (int u = 0; u < PF_SUB; u++) {
+        for (int u = 0; u < SUB; u++) {
             // a 32-position tile is one 32-row block of the ring (rows are a multiple of 32), K and V alike; tiles
             // past the split's end stay inside the plane and are never computed
-            const size_t off = (size_t)((lo + TILE * (PF_SUB * j + u)) % rows) * HD;
-            dma16((const unsigned char*)(K + off) + w * 1024 + lane * 16, dst + u * PF_TILE);
-            dma16((const unsigned char*)(V + off) + w * 1024 + lane * 16, dst + (PF_SUB + u) * PF_TILE);
+            const size_t off = (size_t)((lo + TILE * (SUB * j + u)) % rows) * HD * Gm::BPE + w * (TB / PF_NW) + lane * 16;
+#pragma unroll
+            for (int d = 0; d < Gm::DPT; d++) {
+                dma16(K + off + d * 1024, dst + u * TB + d * 1024);
+                dma16(V + off + d * 1024, dst + (SUB + u) * TB + d * 1024);
+            }
         }
     };
     for (int j = 0; j < PF_NSLOT - 1 && j < ntiles; j++) issue(j);
@@ -350,7 +339,9 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf16(const _Float16* __restrict
             split8(x0, x1, qh[s], ql[s]);
         }
     }
-    const int kaddr = h * 512 + key_perm(r) * 16;
+    // K in a tile: f16 [dims/8][32 keys][8], f32 [dims/4][32 keys][4]; lane (r, h) of step s takes dims 16s + 8h .. +7
+    // of key key_perm(r)
+    const int kaddr = FMT == 1 ? h * 1024 + key_perm(r) * 16 : h * 512 + key_perm(r) * 16;
     float m = NEG_INF, lsum = 0.f;
     f32x16 O[4];
 #pragma unroll
@@ -359,48 +350,74 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf16(const _Float16* __restrict
     // V rows of a slot outside [lo_first, kend) may be other positions' or never written: zero them in LDS so that
     // 0 * V stays finite (K there only meets masked scores)
     auto zero_v = [&](int j) {
-        unsigned short* Vz = (unsigned short*)(ring + (j % PF_NSLOT) * PF_SLOT + PF_SUB * PF_TILE);
-        const int k0 = lo + TILE * PF_SUB * j;
-        for (int i = tid; i < PF_SUB * TILE * HD; i += PF_NW * 64) {
-            const int key = k0 + (i / (8 * HD)) * 8 + (i & 7);  // group i / 1024, position i % 8 in the group
-            if (key < lo_first || key >= kend) Vz[i] = 0;
+        constexpr int EPG = Gm::EPG;
+        unsigned char* Vz = ring + (j % PF_NSLOT) * SLOT + SUB * TB;
+        const int k0 = lo + TILE * SUB * j;
+        for (int i = tid; i < SUB * TILE * HD; i += PF_NW * 64) {
+            const int key = k0 + (i / (EPG * HD)) * EPG + (i % EPG);  // V group i / (EPG * HD), position i % EPG
+            if (key < lo_first || key >= kend) {
+                if constexpr (FMT == 1) ((float*)Vz)[i] = 0.f;
+                else ((unsigned short*)Vz)[i] = 0;
+            }
         }
     };
     for (int j = 0; j < ntiles; j++) {
-        pf_wait<PF_NSLOT - 2>(min(ntiles - 1 - j, PF_NSLOT - 2));
+        pf_wait<PF_NSLOT - 2, Gm::LPT>(min(ntiles - 1 - j, PF_NSLOT - 2));
         lds_barrier();  // slot j is in LDS for every wave; every wave is done with slot j - 1
         if (j + PF_NSLOT - 1 < ntiles) issue(j + PF_NSLOT - 1);  // into the slot of j - 1
-        const int ks0 = lo + TILE * PF_SUB * j;
-        if (ks0 < lo_first || ks0 + TILE * PF_SUB > kend) {
+        const int ks0 = lo + TILE * SUB * j;
+        if (ks0 < lo_first || ks0 + TILE * SUB > kend) {
             zero_v(j);
             lds_barrier();
         }
 #pragma unroll
-        for (int u = 0; u < PF_SUB; u++) {
+        for (int u = 0; u < SUB; u++) {
             const int k0 = ks0 + TILE * u;
             if (k0 >= hi) break;
-            const unsigned char* Ks = ring + (j % PF_NSLOT) * PF_SLOT + u * PF_TILE;
-            const unsigned char* Vs = ring + (j % PF_NSLOT) * PF_SLOT + (PF_SUB + u) * PF_TILE;
-            // two independent chains (hi and lo of Q), added once: back-to-back MFMAs never wait on each other
+            const unsigned char* Ks = ring + (j % PF_NSLOT) * SLOT + u * TB;
+            const unsigned char* Vs = ring + (j % PF_NSLOT) * SLOT + (SUB + u) * TB;
+            // independent chains (Q hi; Q lo and K lo), added once: back-to-back MFMAs never wait on each other
             f32x16 Sh = f32x16{}, Sl = f32x16{};
-            constexpr int KP = 3;  // K operands in flight ahead of the MFMAs
-            half8 kbuf[KP];
+            if constexpr (FMT == 1) {
+                constexpr int KP = 2;  // K operands (two f32x4 each) in flight ahead of the MFMAs
+                f32x4 kb[KP][2];
 #pragma unroll
-            for (int s = 0; s < KP; s++) kbuf[s] = *(const half8*)(Ks + kaddr + s * 1024);
+                for (int s = 0; s < KP; s++) {
+                    kb[s][0] = *(const f32x4*)(Ks + kaddr + s * 2048);
+                    kb[s][1] = *(const f32x4*)(Ks + kaddr + s * 2048 + 512);
+                }
 #pragma unroll
-            for (int s = 0; s < 8; s++) {
-                const half8 ka = kbuf[s % KP];
-                if (s + KP < 8) kbuf[s % KP] = *(const half8*)(Ks + kaddr + (s + KP) * 1024);
-                Sh = mfma32(ka, qh[s], Sh);
-                Sl = mfma32(ka, ql[s], Sl);
+                for (int s = 0; s < 8; s++) {
+                    half8 kh, kl;
+                    split8(kb[s % KP][0], kb[s % KP][1], kh, kl);
+                    if (s + KP < 8) {
+                        kb[s % KP][0] = *(const f32x4*)(Ks + kaddr + (s + KP) * 2048);
+                        kb[s % KP][1] = *(const f32x4*)(Ks + kaddr + (s + KP) * 2048 + 512);
+                    }
+                    Sh = mfma32(kh, qh[s], Sh);
+                    Sl = mfma32(kh, ql[s], Sl);
+                    Sl = mfma32(kl, qh[s], Sl);
+                }
+            } else {
+                constexpr int KP = 3;  // K operands in flight ahead of the MFMAs
+                half8 kbuf[KP];
+#pragma unroll
+                for (int s = 0; s < KP; s++) kbuf[s] = *(const half8*)(Ks + kaddr + s * 1024);
+#pragma unroll
+                for (int s = 0; s < 8; s++) {
+                    const half8 ka = kbuf[s % KP];
+                    if (s + KP < 8) kbuf[s % KP] = *(const half8*)(Ks + kaddr + (s + KP) * 1024);
+                    Sh = mfma32(ka, qh[s], Sh);
+                    Sl = mfma32(ka, ql[s], Sl);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x100, KP, 0);
+#pragma unroll
+                for (int s = 0; s < 8 - KP; s++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 2 * KP, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x100, KP, 0);
-#pragma unroll
-            for (int s = 0; s < 8 - KP; s++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 2 * KP, 0);
             f32x16 S = Sh + Sl;
             // register i of lane (r, h) is key 8h + i (i < 8) or 16 + 8h + i - 8 of the tile for row r
             if (!__all(k0 >= vlo && k0 + TILE <= vhi)) {
@@ -448,17 +465,38 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf16(const _Float16* __restrict
             for (int k = 0; k < 2; k++)
                 split8(f32x4{p[8 * k], p[8 * k + 1], p[8 * k + 2], p[8 * k + 3]},
                        f32x4{p[8 * k + 4], p[8 * k + 5], p[8 * k + 6], p[8 * k + 7]}, ph[k], pl[k]);
-            // key step k: keys 16k + 8h .. +7 = V group 2k + h; dim block nb: dims 32nb + r
-            half8 vb[8];
+            // key step k: keys 16k + 8h .. +7 (f16: V group 2k + h; f32: groups 4k + 2h, +1); dim block nb: 32nb + r
+            if constexpr (FMT == 1) {
+                auto vaddr = [&](int i) { return Vs + (4 * (i >> 2) + 2 * h) * (HD * 16) + (32 * (i & 3) + r) * 16; };
+                constexpr int VP = 2;
+                f32x4 vbuf[VP][2];
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                vb[i] = *(const half8*)(Vs + (2 * (i >> 2) + h) * (HD * 16) + (32 * (i & 3) + r) * 16);
+                for (int i = 0; i < VP; i++) {
+                    vbuf[i][0] = *(const f32x4*)vaddr(i);
+                    vbuf[i][1] = *(const f32x4*)(vaddr(i) + HD * 16);
+                }
 #pragma unroll
-            for (int k = 0; k < 2; k++) {
+                for (int i = 0; i < 8; i++) {
+                    half8 vh, vl;
+                    split8(vbuf[i % VP][0], vbuf[i % VP][1], vh, vl);
+                    if (i + VP < 8) {
+                        vbuf[i % VP][0] = *(const f32x4*)vaddr(i + VP);
+                        vbuf[i % VP][1] = *(const f32x4*)(vaddr(i + VP) + HD * 16);
+                    }
+                    O[i & 3] = mfma32(pl[i >> 2], vh, mfma32(ph[i >> 2], vl, mfma32(ph[i >> 2], vh, O[i & 3])));
+                }
+            } else {
+                half8 vb[8];
 #pragma unroll
-                for (int nb = 0; nb < 4; nb++) O[nb] = mfma32(ph[k], vb[4 * k + nb], O[nb]);
+                for (int i = 0; i < 8; i++)
+                    vb[i] = *(const half8*)(Vs + (2 * (i >> 2) + h) * (HD * 16) + (32 * (i & 3) + r) * 16);
 #pragma unroll
-                for (int nb = 0; nb < 4; nb++) O[nb] = mfma32(pl[k], vb[4 * k + nb], O[nb]);
+                for (int k = 0; k < 2; k++) {
+#pragma unroll
+                    for (int nb = 0; nb < 4; nb++) O[nb] = mfma32(ph[k], vb[4 * k + nb], O[nb]);
+#pragma unroll
+                    for (int nb = 0; nb < 4; nb++) O[nb] = mfma32(pl[k], vb[4 * k + nb], O[nb]);
+                }
             }
         }
     }
@@ -858,7 +896,7 @@ __global__ void __launch_bounds__(256) fl_merge_few(const float* __restrict__ pa
 
 }  // namespace
 
-Plan plan(int fmt, int pos0, int T, int win) {
+Plan plan(int pos0, int T, int win) {
     const int lo0 = win > 0 && pos0 + 1 > win ? pos0 + 1 - win : 0;
     const int klo = lo0 / 32 * 32, span = pos0 + T - klo;
     int nrb = (T + 3) / 4;
@@ -869,16 +907,12 @@ Plan plan(int fmt, int pos0, int T, int win) {
     } else if (T <= 4) {  // one block of fl_attn: splits of at least 128 positions, 64 per kv head at most
         nch = span / 128;
         nch = nch > 64 ? 64 : nch;
-    } else if (fmt == 0) {  // fl_pf16: blocks of 32 tokens, about one work-group per CU, splits of 64 positions or more
+    } else {  // fl_pf: blocks of 32 tokens, about one work-group per CU, splits of 64 positions or more
         nrb = (T + PF_PT - 1) / PF_PT;
         nch = 256 / (nrb * KVH);
         const int most = span / 64, room = WS_ROWS / (T * GQA);
         nch = nch > most ? most : nch;
         nch = nch > room ? room : nch > 16 ? 16 : nch;
-    } else {
-        nch = 512 / (nrb * KVH);
-        const int most = span / 128;
-        nch = nch > most ? most : nch > 16 ? 16 : nch;
     }
     nch = nch < 1 ? 1 : nch;
     return Plan{klo, span, nch, nrb};
@@ -899,17 +933,16 @@ hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const 
                               win, scale2, p.klo, p.span, p.nch, ws)
                      : launch(fl_dec16<0, FL_DEC_BUF>, dim3(p.nch * KVH), dim3(256), L, kp, vp, pe, rows, q, T, pos0,
                               win, scale2, p.klo, p.span, p.nch, ws);
-    else if (fmt == 1)  // blocks of 4 tokens: one wave group for 3-4 tokens, two for prefill
-        e = T <= 4 ? launch(fl_attn<1, 1, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
-                            p.span, p.nch, p.nrb, ws)
-                   : launch(fl_attn<1, 2, 2>, grid, dim3(512), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
-                            p.span, p.nch, p.nrb, ws);
-    else if (T <= 4)
-        e = launch(fl_attn<0, 1, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo, p.span,
-                   p.nch, p.nrb, ws);
-    else  // f16 prefill: 32-token blocks over an LDS ring
-        e = launch(fl_pf16, grid, dim3(PF_NW * 64), L, (const _Float16*)kp, (const _Float16*)vp, pe, rows, q, T, pos0,
-                   win, scale2, p.klo, p.span, p.nch, ws);
+    else if (T <= 4)  // one block of 4 tokens
+        e = fmt == 1 ? launch(fl_attn<1, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
+                              p.span, p.nch, p.nrb, ws)
+                     : launch(fl_attn<0, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
+                              p.span, p.nch, p.nrb, ws);
+    else  // prefill: 32-token blocks over an LDS ring
+        e = fmt == 1 ? launch(fl_pf<1>, grid, dim3(PF_NW * 64), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
+                              p.span, p.nch, ws)
+                     : launch(fl_pf<0>, grid, dim3(PF_NW * 64), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
+                              p.span, p.nch, ws);
     if (e != hipSuccess) return e;
     if (p.nch > 8 * MERGE_J) return hipErrorInvalidValue;
     if (p.nch <= MERGE_FEW)
