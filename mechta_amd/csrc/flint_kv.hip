@@ -666,11 +666,51 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
                                                 float* __restrict__ part) {
     constexpr int BPE = FMT == 1 ? 4 : 2;
     const int c = blockIdx.x % nch, kvh = blockIdx.x / nch;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: subtile addressing stays scalar
     const int lo_first = window_lo(pos0, win);
     const int cs = klo + chunk_lo(c, span, nch), ce = c + 1 < nch ? klo + chunk_lo(c + 1, span, nch) : klo + span;
     const int lo = max(cs, lo_first / TILE * TILE), hi = min(ce, pos0 + T);
     const int nsub = hi > lo ? (hi - lo + 15) / 16 : 0;
+
+    const unsigned pbytes = (unsigned)(plane_elems * BPE);
+    const rsrc_t kr = plane_rsrc((const char*)kplane + (size_t)kvh * plane_elems * BPE, pbytes);
+    const rsrc_t vr = plane_rsrc((const char*)vplane + (size_t)kvh * plane_elems * BPE, pbytes);
+    // the subtile's offset is wave-uniform and goes in the scalar operand; the lane offsets stay fixed, so the loop
+    // writes no vector register for addresses (a pending load's destination is never reused for them)
+    auto load = [&](SubRegs<FMT>& X, int j) {
+        const int r0 = (lo + 16 * (j < nsub ? j : 0)) % rows;  // past the last: any subtile (never computed)
+        const unsigned blk = (unsigned)(r0 / 32) * (32 * HD * BPE), sub = r0 % 32;
+        const unsigned sk = __builtin_amdgcn_readfirstlane(blk + sub * 16);
+        const unsigned sv = __builtin_amdgcn_readfirstlane(blk + (sub / (16 / BPE)) * HD * 16);
+        if constexpr (FMT == 1) {
+#pragma unroll
+            for (int a = 0; a < 8; a++)
+                X.k[a] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                    kr, ((8 * (a >> 1) + 2 * g + (a & 1)) * 32 + r16) * 16, sk, LOAD_NT));
+#pragma unroll
+            for (int cc = 0; cc < 8; cc++)
+                X.v[cc] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        vr, (g * HD + 16 * cc + r16) * 16, sv, LOAD_NT));
+        } else {
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+                X.k[a] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       kr, ((4 * a + g) * 32 + r16) * 16, sk, LOAD_NT));
+#pragma unroll
+            for (int cc = 0; cc < 8; cc++)
+                X.v[cc] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(
+                                                        vr, ((g >> 1) * HD * 8 + (16 * cc + r16) * 8 + 4 * (g & 1)) * 2,
+                                                        sv, 0));
+        }
+    };
+
+    // the first subtiles' loads go out before Q's, so the two latencies overlap
+    const int mine = nsub > w ? (nsub - w + 3) / 4 : 0;  // this wave's subtiles w, w + 4, ...
+    SubRegs<FMT> R[NBUF];
+#pragma unroll
+    for (int k = 0; k < NBUF - 1; k++) load(R[k], w + 4 * k);
+    __builtin_amdgcn_sched_barrier(0);
 
     // Q of the lane's row in registers, split into f16 hi + lo: step a holds dims 32a + 8g .. +7 (the B operand)
     half8 qh[4], ql[4];
@@ -684,38 +724,6 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
             split8(x0, x1, qh[a], ql[a]);
         }
     }
-    const unsigned pbytes = (unsigned)(plane_elems * BPE);
-    const rsrc_t kr = plane_rsrc((const char*)kplane + (size_t)kvh * plane_elems * BPE, pbytes);
-    const rsrc_t vr = plane_rsrc((const char*)vplane + (size_t)kvh * plane_elems * BPE, pbytes);
-    auto load = [&](SubRegs<FMT>& X, int j) {
-        unsigned blk = pbytes;  // subtiles past the last: every offset lies past the plane (zeros)
-        int sub = 0;
-        if (j < nsub) {
-            const int r0 = (lo + 16 * j) % rows;
-            blk = (unsigned)(r0 / 32) * (32 * HD * BPE);
-            sub = r0 % 32;
-        }
-        if constexpr (FMT == 1) {
-#pragma unroll
-            for (int a = 0; a < 8; a++)
-                X.k[a] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                    kr, blk + ((8 * (a >> 1) + 2 * g + (a & 1)) * 32 + sub + r16) * 16, 0, LOAD_NT));
-#pragma unroll
-            for (int cc = 0; cc < 8; cc++)
-                X.v[cc] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        vr, blk + ((sub / 4 + g) * HD + 16 * cc + r16) * 16, 0, LOAD_NT));
-        } else {
-#pragma unroll
-            for (int a = 0; a < 4; a++) X.k[a] = bload16(kr, blk + ((4 * a + g) * 32 + sub + r16) * 16);
-            const int rr = sub + 4 * g;
-#pragma unroll
-            for (int cc = 0; cc < 8; cc++)
-                X.v[cc] = __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(
-                                                        vr, blk + ((rr / 8) * HD * 8 + (16 * cc + r16) * 8 + rr % 8) * 2,
-                                                        0, 0));
-        }
-    };
-
     const int prow = pos0 + (r16 >> 3);
     const int plo = window_lo(prow, win);
     float m_run = NEG_INF, l_run = 0.f;
@@ -798,15 +806,12 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
         }
     };
 
-    const int mine = nsub > w ? (nsub - w + 3) / 4 : 0;  // this wave's subtiles w, w + 4, ...
-    SubRegs<FMT> R[NBUF];
-#pragma unroll
-    for (int k = 0; k < NBUF - 1; k++) load(R[k], w + 4 * k);
     for (int i0 = 0; i0 < mine; i0 += NBUF) {
 #pragma unroll
         for (int k = 0; k < NBUF; k++) {
             if (i0 + k < mine) {  // uniform in the wave
                 load(R[(k + NBUF - 1) % NBUF], w + 4 * (i0 + k + NBUF - 1));
+                __builtin_amdgcn_sched_barrier(0);  // the next subtile's loads issue before this one's wait
                 step(R[k], w + 4 * (i0 + k));
             }
         }
