@@ -912,12 +912,12 @@ Plan plan(int pos0, int T, int win) {
     } else if (T <= 4) {  // one block of fl_attn: splits of at least 128 positions, 64 per kv head at most
         nch = span / 128;
         nch = nch > 64 ? 64 : nch;
-    } else {  // fl_pf: blocks of 32 tokens, about one work-group per CU, splits of 64 positions or more
+    } else {  // fl_pf: blocks of 32 tokens, about one work-group per CU, splits of 64 positions or more, at most 64
         nrb = (T + PF_PT - 1) / PF_PT;
         nch = 256 / (nrb * KVH);
         const int most = span / 64, room = WS_ROWS / (T * GQA);
         nch = nch > most ? most : nch;
-        nch = nch > room ? room : nch > 16 ? 16 : nch;
+        nch = nch > room ? room : nch > 64 ? 64 : nch;
     }
     nch = nch < 1 ? 1 : nch;
     return Plan{klo, span, nch, nrb};
