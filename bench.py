@@ -338,6 +338,7 @@ def bench_cfg5(torch, mk, reps=3):
         return outs
 
     before = verify(a)
+    a.snapshot(p, host)  # untimed: the process's first device-to-host copy pays a one-time set-up (about 13% slower)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(reps):
@@ -345,6 +346,8 @@ def bench_cfg5(torch, mk, reps=3):
     t_snap = (time.perf_counter() - t0) / reps
     a.close()
     b = mk.KvStore(L, 17408, mk.F32)
+    b.restore(p, host)  # untimed, as the snapshot
+    b.sync()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(reps):
