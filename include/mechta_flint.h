@@ -36,7 +36,8 @@ typedef struct mfl_store mfl_t;
 
 /* Allocates the K/V of `layers` layers, zero filled: layer l holds 1024 rows if sliding[l] != 0, else ctx rows.
  * ctx: a multiple of 1024 in [1024, 262144]; fmt: MKV_F32 (the reference's default) or MKV_F16 (MECHTA_FLINT_KV=f16,
- * flint.rs:72-90). Replaces the kc / vc buffers of Flint::new (flint.rs:227-232). */
+ * flint.rs:72-90). Replaces the kc / vc buffers of Flint::new (flint.rs:227-232). The handle also holds the
+ * attention's split partials, 34.6 MB, allocated here, so attention calls never allocate. */
 int mfl_create(mfl_t** out, int layers, int ctx, int fmt, const unsigned char* sliding, void* stream);
 int mfl_destroy(mfl_t* h);
 int mfl_set_stream(mfl_t* h, void* stream);
