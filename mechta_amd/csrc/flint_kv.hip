@@ -3,10 +3,10 @@
 //
 // Three attention kernels: fl_dec16 (1-2 tokens, 16 query rows), fl_attn (3-4 tokens) and fl_pf (prefill blocks of
 // 5-512 tokens, 32 tokens per work-group sharing an LDS ring of K/V tiles). fl_attn's work-group: (block of 4 tokens,
-// key split, kv head) = 32 query rows (token * 8 + head) against the split's keys in tiles of 32 positions. The arithmetic is f32, as the reference's, taken on the f16 matrix units: f32
-// operands are split into f16 hi + lo and each product is three v_mfma_f32_32x32x16_f16 passes (hi.hi + hi.lo +
-// lo.hi, f32 accumulation), two where one side is an f16 cache's K or V (exact in f16). Per tile, wave w of a group
-// of 4:
+// key split, kv head) = 32 query rows (token * 8 + head) against the split's keys in tiles of 32 positions. The
+// arithmetic is f32, as the reference's, taken on the f16 matrix units: f32 operands are split into f16 hi + lo and
+// each product is three v_mfma_f32_32x32x16_f16 passes (hi.hi + hi.lo + lo.hi, f32 accumulation), two where one side
+// is an f16 cache's K or V (exact in f16). Per tile, wave w of 4:
 //   S^T[32 keys][32 rows] over dims 32w .. 32w+31    2 dim steps, A = K straight from HBM, B = Q (split once, LDS)
 //   the four partial S^T summed through LDS in one order, exact-max online softmax (redundantly in every wave)
 //   O[32 rows][dims 32w .. 32w+31] += P . V           2 key steps, A = P (split from the S^T registers), B = V
@@ -57,9 +57,9 @@ struct TileRegs<0> {  // f16: K dims 32w + 16a + 8s .. +7 (a < 2); V keys 8q + 4
 
 template <int FMT, int NBUF>  // NBUF: tiles in registers (NBUF - 1 in flight ahead of the one computed)
 __global__ void __launch_bounds__(256) fl_attn(const void* __restrict__ kplane, const void* __restrict__ vplane,
-                                                     size_t plane_elems, int rows, const float* __restrict__ q, int T,
-                                                     int pos0, int win, float scale2, int klo, int span, int nch,
-                                                     int nrb, float* __restrict__ part) {
+                                               size_t plane_elems, int rows, const float* __restrict__ q, int T,
+                                               int pos0, int win, float scale2, int klo, int span, int nch, int nrb,
+                                               float* __restrict__ part) {
     constexpr int BPE = FMT == 1 ? 4 : 2;
     constexpr unsigned TILE_BYTES = TILE * HD * BPE;
     const int G = gridDim.x, L = blockIdx.x;
@@ -315,7 +315,8 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
         for (int u = 0; u < SUB; u++) {
             // a 32-position tile is one 32-row block of the ring (rows are a multiple of 32), K and V alike; tiles
             // past the split's end stay inside the plane and are never computed
-            const size_t off = (size_t)((lo + TILE * (SUB * j + u)) % rows) * HD * Gm::BPE + w * (TB / PF_NW) + lane * 16;
+            const size_t off =
+                (size_t)((lo + TILE * (SUB * j + u)) % rows) * HD * Gm::BPE + w * (TB / PF_NW) + lane * 16;
 #pragma unroll
             for (int d = 0; d < Gm::DPT; d++) {
                 dma16(K + off + d * 1024, dst + u * TB + d * 1024);
