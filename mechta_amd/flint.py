@@ -91,6 +91,10 @@ class FlintStore:
         except Exception:
             pass
 
+    def set_stream(self, stream):
+        """Later calls enqueue on `stream` (a torch.cuda.Stream), e.g. torch's stream while capturing a graph."""
+        _check(lib().mfl_set_stream(self._h, ctypes.c_void_p(stream.cuda_stream)))
+
     def sync(self):
         _check(lib().mfl_sync(self._h))
 

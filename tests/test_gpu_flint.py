@@ -178,3 +178,53 @@ def test_nan_rows_outside_the_window(torch_gpu, mf, fmt):
             outd = st.attend(layer, pos0 + T - 1, dev(torch, q[-1:]), dev(torch, sinks)).cpu().numpy()
             assert_attn_close(outd[0], O.fl_attn_fd(fmt, kc, vc, q[-1], pos0 + T - 1, win, sinks), atol=TOL,
                               rtol=TOL, what=f"decode layer {layer} next to NaN rows")
+
+
+@pytest.mark.parametrize("fmt", [F32, F16])
+def test_captured_step_replay_bit_identical(torch_gpu, mf, fmt):
+    """A Flint step under HIP graph capture (the reference records its commands once, flint.rs builds them per step
+    shape): ring append of a 64-token block and its prefill attention on a sliding and a full layer, then a one-token
+    decode on each. Attention and append allocate nothing after create, so no eager call precedes the capture. Every
+    replay equals the eager step bit for bit (replays re-append the same rows), with eager attention of the same
+    store between replays."""
+    torch = torch_gpu
+    print(f"flint graph capture fmt={fmt}", flush=True)
+    pos0, T = 1500, 64
+    with mf.FlintStore(2, 4096, fmt, sliding=[True, False]) as st:
+        for layer in (0, 1):
+            kc, vc = O.fl_new_cache(st.rows(layer), fmt), O.fl_new_cache(st.rows(layer), fmt)
+            fill(torch, st, kc, vc, layer, fmt, pos0, seed=50 + layer)
+        r = rng(52)
+        k, v = (dev(torch, r.standard_normal((T, KVH, D), dtype=np.float32)) for _ in range(2))
+        q = dev(torch, r.standard_normal((T, H, D), dtype=np.float32))
+        q1 = dev(torch, r.standard_normal((1, H, D), dtype=np.float32))
+        sinks = dev(torch, r.standard_normal(H, dtype=np.float32))
+
+        def step(outs):
+            for layer in (0, 1):
+                st.append(layer, pos0, k, v)
+                st.attend(layer, pos0, q, sinks, out=outs[2 * layer])
+                st.attend(layer, pos0 + T - 1, q1, sinks, out=outs[2 * layer + 1])
+
+        shapes = [(T, H, D), (1, H, D)] * 2
+        eager = [torch.empty(s, dtype=torch.float32, device="cuda") for s in shapes]
+        step(eager)
+        torch.cuda.synchronize()
+        outs = [torch.empty_like(x) for x in eager]
+        g = torch.cuda.CUDAGraph()
+        base_stream = torch.cuda.current_stream()
+        with torch.cuda.graph(g):
+            st.set_stream(torch.cuda.current_stream())
+            step(outs)
+        st.set_stream(base_stream)
+        torch.cuda.synchronize()
+        for rep in range(4):
+            for x in outs:
+                x.fill_(float("nan"))
+            g.replay()
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(zip(outs, eager)):
+                assert torch.equal(a, b), f"replay {rep}: output {i} differs from the eager step"
+            st.attend(1, 700, q1, sinks)  # eager work of the same store between replays
+            st.attend(0, pos0 - 1, q, sinks)
+            torch.cuda.synchronize()
