@@ -1,11 +1,9 @@
-// kv_attn32.hip -- attention over the f32 store on the fp32 matrix cores: the decode of 1-4 tokens (the reference's
-// exact-f32 attn_fd applied per token with the drafts' causal mask, ops.wgsl:310-394, quad.rs:127-131) and the block
-// prefill (attn_fa, ops.wgsl:540-651), one kernel for both.
+// kv_attn32.hip -- decode attention over the f32 store: 1-4 tokens (the reference's exact-f32 attn_fd applied per
+// token with the drafts' causal mask, ops.wgsl:310-394, quad.rs:127-131), with the fused append. The f32 store's
+// prefill is prefill_f32 (kv_prefill.hip).
 //
 // Work-group (block of 4 tokens, key split, kv head): 32 query rows (token * 8 + head) against the split's keys in
-// tiles of 32 keys, by NWG groups of 4 waves that take alternate tiles. Prefill runs two groups (two waves per SIMD:
-// one group's MFMAs run while the other waits for its loads; their states are merged through LDS at the end). Decode
-// runs one: its splits are only 4-5 tiles long, too few to share.
+// tiles of 32 keys, by 4 waves.
 //
 // f32 products on the f16 matrix units: each f32 operand x is split into hi = f16(x) and lo = f16(x - hi), and a
 // product a.b is taken as hi(a)hi(b) + hi(a)lo(b) + lo(a)hi(b) (three v_mfma_f32_32x32x16_f16, f32 accumulation; the
@@ -42,10 +40,10 @@ struct Tile {
     f32x4 v[8];  // V: keys 16k + 8e + 4s .. +3 of dim 64w + 32c + l % 32 (index 4k + 2c + e)
 };
 
-// NWG wave groups; NBUF tiles in registers, NBUF - 1 of them loading while one computes (2: deeper prefetch measured
-// slower from HBM, 3 tiles 2 us and 4 tiles 5 us more per 16K-position decode)
-template <int NWG, int NBUF>
-__global__ void __launch_bounds__(256 * NWG, 2) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
+// NBUF tiles in registers, NBUF - 1 of them loading while one computes (2: deeper prefetch measured slower from HBM,
+// 3 tiles 2 us and 4 tiles 5 us more per 16K-position decode)
+template <int NBUF>
+__global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
                                                 size_t plane_elems, const float* __restrict__ q, int T, int n,
                                                 int start, float scale2, int span, int nch, int c0, int nrb, int rpk,
                                                 float* __restrict__ part, const float* __restrict__ akn,
@@ -57,7 +55,7 @@ __global__ void __launch_bounds__(256 * NWG, 2) attn_f32(const float* __restrict
     const int W = G % NXCD == 0 ? (L % NXCD) * (G / NXCD) + L / NXCD : L;
     const int ncg = nch - c0;
     const int rb = W % nrb, c = c0 + (W / nrb) % ncg, kvh = W / nrb / ncg;
-    const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 8, w = (tid >> 6) & 3, s = lane >> 5, r32 = lane & 31;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, s = lane >> 5, r32 = lane & 31;
     const int t0 = 4 * rb, nt = min(4, T - t0);
     const int kend = n + T - 1;  // keys of the whole call
     // span > 0: work-group c takes the contiguous split [chunk_lo(c), chunk_lo(c + 1)) (prefill: the token blocks of
@@ -92,7 +90,7 @@ __global__ void __launch_bounds__(256 * NWG, 2) attn_f32(const float* __restrict
                 apf = apl == 0 ? p : apf;
                 apl = p + 1;
             }
-        for (int i = tid; i < (apl - apf) * HD; i += 256 * NWG) {
+        for (int i = tid; i < (apl - apf) * HD; i += 256) {
             const int t = apf - apos + i / HD, d = i % HD;
             newk[i / HD][d] = rope_dim(akn + ((size_t)t * KVH + kvh) * HD, atab + (size_t)t * 64, d);
             newv[i / HD][d] = av[(size_t)t * (KVH * HD) + kvh * HD + d];
@@ -100,8 +98,8 @@ __global__ void __launch_bounds__(256 * NWG, 2) attn_f32(const float* __restrict
     }
 
     __shared__ __attribute__((aligned(16))) _Float16 qh[ROWS][QPAD], ql[ROWS][QPAD];  // Q split: hi, lo
-    __shared__ f32x4 sx[2][NWG][4][4][64];  // partial S^T: [tile parity][group][wave][register quad][lane]
-    for (int i = tid; i < ROWS * HD / 8; i += 256 * NWG) {
+    __shared__ f32x4 sx[2][4][4][64];  // partial S^T: [tile parity][wave][register quad][lane]
+    for (int i = tid; i < ROWS * HD / 8; i += 256) {
         const int row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
         f32x4 x0 = f32x4{}, x1 = f32x4{};
         if (t < T) {
@@ -161,8 +159,7 @@ __global__ void __launch_bounds__(256 * NWG, 2) attn_f32(const float* __restrict
             const half8 bl = *(const half8*)&ql[r32][64 * w + 16 * k + 8 * s];
             S = mfma3(kh, kl, bh, bl, S);
         }
-        const int pb = (j / NWG) & 1;
-        f32x4(&sg)[4][4][64] = sx[pb][grp];
+        f32x4(&sg)[4][4][64] = sx[j & 1];
 #pragma unroll
         for (int a = 0; a < 4; a++) sg[w][a][lane] = f32x4{S[4 * a], S[4 * a + 1], S[4 * a + 2], S[4 * a + 3]};
         lds_barrier();  // parity buffers: a group's round i + 2 writes pb again only after every wave passed round i + 1
@@ -226,18 +223,16 @@ __global__ void __launch_bounds__(256 * NWG, 2) attn_f32(const float* __restrict
         }
     };
 
-    // group g takes tiles g, g + 2, ...; both run the same number of rounds (every wave meets every barrier): a round
-    // past the last tile loads nothing (zeros) and has every key masked
-    const int rounds = (ntile + NWG - 1) / NWG;
+    const int rounds = ntile;
     Tile X[NBUF];
 #pragma unroll
-    for (int b = 0; b < NBUF - 1; b++) load(X[b], b * NWG + grp);
+    for (int b = 0; b < NBUF - 1; b++) load(X[b], b);
     for (int i = 0; i < rounds; i += NBUF) {
 #pragma unroll
         for (int b = 0; b < NBUF; b++) {
             if (i + b >= rounds) break;
-            load(X[(b + NBUF - 1) % NBUF], (i + b + NBUF - 1) * NWG + grp);
-            step(X[b], (i + b) * NWG + grp);
+            load(X[(b + NBUF - 1) % NBUF], i + b + NBUF - 1);
+            step(X[b], i + b);
         }
     }
 
@@ -245,44 +240,10 @@ __global__ void __launch_bounds__(256 * NWG, 2) attn_f32(const float* __restrict
     if (apl > apf) {
         float* Kp = (float*)kplane + (size_t)kvh * plane_elems;
         float* Vp = (float*)vplane + (size_t)kvh * plane_elems;
-        for (int i = tid; i < (apl - apf) * HD; i += 256 * NWG) {
+        for (int i = tid; i < (apl - apf) * HD; i += 256) {
             const int r = i / HD, d = i % HD;
             Kp[k_off32(apf + r, d)] = newk[r][d];
             Vp[v_off32(apf + r, d)] = newv[r][d];
-        }
-    }
-
-    // merge group 1 into group 0 through LDS (the parity buffers are free after the barrier)
-    if constexpr (NWG == 2) {
-        __syncthreads();
-        float* ob = (float*)&sx[0][0][0][0][0];  // [wave][2][16][64] O of group 1, then m, l of its 32 rows
-        float* ml = ob + 4 * 2 * 16 * 64;
-        if (grp == 1) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                ob[((w * 2 + 0) * 16 + i) * 64 + lane] = O[0][i];
-                ob[((w * 2 + 1) * 16 + i) * 64 + lane] = O[1][i];
-            }
-            if (w == 0 && s == 0) {
-                ml[r32] = m_run;
-                ml[32 + r32] = l_run;
-            }
-        }
-        __syncthreads();
-        if (grp == 1) return;
-        {
-            const float m1 = ml[r32], l1 = ml[32 + r32];
-            const float M = fmaxf(m_run, m1);
-            const float f0 = m_run == NEG_INF ? 0.f : exp2f(m_run - M), f1 = m1 == NEG_INF ? 0.f : exp2f(m1 - M);
-            l_run = l_run * f0 + l1 * f1;
-            m_run = M;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int row = 8 * (i >> 2) + 4 * s + (i & 3);
-                const float g0 = __shfl(f0, row), g1 = __shfl(f1, row);
-                O[0][i] = O[0][i] * g0 + ob[((w * 2 + 0) * 16 + i) * 64 + lane] * g1;
-                O[1][i] = O[1][i] * g0 + ob[((w * 2 + 1) * 16 + i) * 64 + lane] * g1;
-            }
         }
     }
 
@@ -307,26 +268,14 @@ __global__ void __launch_bounds__(256 * NWG, 2) attn_f32(const float* __restrict
 }  // namespace
 
 Attn32Plan attn32_plan(int T, int n, int start) {
+    // the window's tiles dealt round robin to at most 248 work-groups per kv head, at least 4 tiles each; two
+    // work-groups per CU (registers held to 256 per lane for two waves per SIMD): at 16,384 positions the core takes
+    // 21.9 us against 24.0 us with one work-group per CU (124 per kv head). Every work-group holds keys of every row,
+    // so the merge reads all (span 0)
     const int kend = n + T - 1;
-    const int nrb = (T + 3) / 4;
-    if (T <= 4) {
-        // decode: the window's tiles dealt round robin to at most 248 work-groups per kv head, at least 4 tiles each;
-        // two work-groups per CU (registers held to 256 per lane for two waves per SIMD): at 16,384 positions the core
-        // takes 21.9 us against 24.0 us with one work-group per CU (124 per kv head). Every work-group holds keys of
-        // every row, so the merge reads all (span 0)
-        int nch = (kend - start / TILE * TILE) / 128;
-        nch = nch > 248 ? 248 : nch < 1 ? 1 : nch;
-        return Attn32Plan{0, nch, 0, nrb};
-    }
-    // prefill: contiguous splits, about two work-groups per CU, splits of at least 128 positions, at most 16 (one
-    // merge round trip)
-    int nch = 512 / (nrb * KVH);
-    const int most = kend / 128;
-    nch = nch > most ? most : nch > 16 ? 16 : nch;
-    nch = nch < 1 ? 1 : nch;
-    int c0, c1;  // splits wholly below `start` get no work-group
-    chunk_range(start, kend, kend, nch, c0, c1);
-    return Attn32Plan{kend, nch, c0, nrb};
+    int nch = (kend - start / TILE * TILE) / 128;
+    nch = nch > 248 ? 248 : nch < 1 ? 1 : nch;
+    return Attn32Plan{0, nch, 0, (T + 3) / 4};
 }
 
 hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
@@ -337,11 +286,9 @@ hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const flo
     const char* b = (const char*)base;
     const float* kp = (const float*)(b + g.plane(layer, 0, 0) * g.plane_bytes());
     const float* vp = (const float*)(b + g.plane(layer, 1, 0) * g.plane_bytes());
+    if (T > 4) return hipErrorInvalidValue;  // decode only: prefill_f32 serves blocks
     dim3 grid(p.nrb * (p.nch - p.c0) * KVH);
-    if (T <= 4)
-        return launch(attn_f32<1, 2>, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
-                      p.nch, p.c0, p.nrb, rpk, part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
-    return launch(attn_f32<2, 2>, grid, dim3(512), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
+    return launch(attn_f32<2>, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
                   p.nch, p.c0, p.nrb, rpk, part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
 }
 

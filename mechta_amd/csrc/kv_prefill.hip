@@ -266,6 +266,196 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
     }
 }
 
+
+// ---- f32 store: causal prefill with f32-class arithmetic (attn_fa, ops.wgsl:540-651) ----
+// Work-group = (16 tokens of the block, key split, kv head), 8 waves: wave w takes row block w / 2 (4 tokens x 8
+// heads = 32 rows) and dim half w % 2 (128 dims). The split's 32-key tiles (32 KB of K, 32 KB of V) stream through a
+// 2-slot LDS ring filled by direct global->LDS loads and shared by the 8 waves, so a key is fetched once per 16
+// tokens. f32 operands are split into f16 hi + lo (hi.hi + hi.lo + lo.hi on v_mfma_f32_32x32x16_f16). Per tile and
+// wave:
+//   partial S^T[32 keys][32 rows] over the wave's 128 dims: 8 dim steps x 3 passes (A = K rows in key_perm order,
+//   split as they leave LDS; B = Q split once, in registers); the two halves are exchanged through LDS and added
+//   (a + b in both waves, so both hold the same S)
+//   online softmax with a lazy reference max, redundantly in both waves of the pair
+//   O[32 rows][the wave's 128 dims] += P . V: 2 key steps x 4 dim blocks x 3 passes
+// Registers hold Q's hi and lo for 128 dims and O for 128 dims; LDS is 128 KB of ring and 32 KB of S exchange.
+constexpr int P32_NW = 8;
+constexpr int P32_PT = 16;                    // tokens per work-group
+constexpr int P32_TILE = 32 * HD * 4;         // f32 K (or V) bytes of 32 positions: 32 KB
+constexpr int P32_SLOT = 2 * P32_TILE;
+constexpr int P32_LPT = P32_SLOT / P32_NW / 1024;  // direct loads per wave and slot: 8
+
+__global__ void __launch_bounds__(P32_NW * 64) prefill_f32(const float* __restrict__ kplane,
+                                                          const float* __restrict__ vplane, size_t plane_elems,
+                                                          const float* __restrict__ q, int T, int n, int start,
+                                                          float scale2, int span, int nch, float* __restrict__ part) {
+    const int G = gridDim.x, Lb = blockIdx.x;
+    const int W = G % NXCD == 0 ? (Lb % NXCD) * (G / NXCD) + Lb / NXCD : Lb;
+    const int nblk = (T + P32_PT - 1) / P32_PT;
+    const int rb = W % nblk, sp = (W / nblk) % nch, kvh = W / nblk / nch, tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, h = lane >> 5, r = lane & 31, blk = w >> 1, dh = w & 1;
+    const int t0 = rb * P32_PT + 4 * blk;  // this wave's first token
+    const int tlast = min(T - 1, rb * P32_PT + P32_PT - 1);
+    const int kend = n + T - 1;            // positions written for this block
+    const int cs = chunk_lo(sp, span, nch), ce = min(sp + 1 < nch ? chunk_lo(sp + 1, span, nch) : span, n + tlast);
+    const int ntiles = ce > cs ? (ce - cs + 31) / 32 : 0;
+    const unsigned char* K = (const unsigned char*)(kplane + (size_t)kvh * plane_elems);
+    const unsigned char* V = (const unsigned char*)(vplane + (size_t)kvh * plane_elems);
+
+    __shared__ __attribute__((aligned(16))) unsigned char ring[2 * P32_SLOT];
+    __shared__ __attribute__((aligned(16))) f32x4 xs[P32_NW][4][64];  // each wave's partial S^T
+    auto issue = [&](int j) {  // each wave copies 1/8 of tile j's K and V into slot j % 2
+        const size_t off = (size_t)(cs + 32 * j) * HD * 4 + w * (P32_TILE / P32_NW) + lane * 16;
+        unsigned char* dst = ring + (j & 1) * P32_SLOT + w * (P32_TILE / P32_NW);
+#pragma unroll
+        for (int d = 0; d < P32_TILE / P32_NW / 1024; d++) {
+            dma16(K + off + d * 1024, dst + d * 1024);
+            dma16(V + off + d * 1024, dst + P32_TILE + d * 1024);
+        }
+    };
+    if (ntiles > 0) issue(0);
+
+    // Q: lane (r, h) holds row r (token t0 + r / 8, head r % 8), dims 128dh + 16s + 8h .. +7 of step s, split
+    const int tr = t0 + (r >> 3);
+    const int vis = tr < T ? n + tr : 0;  // row r sees keys [start, vis)
+    half8 qh[8], ql[8];
+    {
+        const float* qrow = q + ((size_t)min(tr, T - 1) * QH + kvh * GQA + (r & 7)) * HD + 128 * dh + 8 * h;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            f32x4 x0 = *(const f32x4*)(qrow + 16 * s), x1 = *(const f32x4*)(qrow + 16 * s + 4);
+            if (tr >= T) x0 = x1 = f32x4{};
+            split8(x0, x1, qh[s], ql[s]);
+        }
+    }
+    const int kaddr = (32 * dh + 2 * h) * 512 + key_perm(r) * 16;  // K chunk (dims / 4) 32dh + 4s + 2h, +1
+    float m = NEG_INF, lsum = 0.f;
+    f32x16 O[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) O[nb] = f32x16{};
+
+    for (int j = 0; j < ntiles; j++) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();  // tile j is in LDS for every wave; every wave is done with tile j - 1 and its S exchange
+        if (j + 1 < ntiles) issue(j + 1);  // into the slot of tile j - 1
+        const int k0 = cs + 32 * j;
+        const unsigned char* Ks = ring + (j & 1) * P32_SLOT;
+        const unsigned char* Vs = Ks + P32_TILE;
+        if (k0 + 32 > kend) {  // V rows past the written length may hold anything: zero them (0 * V stays finite)
+            float* Vz = (float*)Vs;
+            for (int i = tid; i < 32 * HD; i += P32_NW * 64)
+                if (k0 + (i / (4 * HD)) * 4 + (i & 3) >= kend) Vz[i] = 0.f;
+            lds_barrier();
+        }
+        f32x16 Sh = f32x16{}, Sl = f32x16{};
+        constexpr int KP = 2;
+        f32x4 kb[KP][2];
+#pragma unroll
+        for (int s = 0; s < KP; s++) {
+            kb[s][0] = *(const f32x4*)(Ks + kaddr + s * 2048);
+            kb[s][1] = *(const f32x4*)(Ks + kaddr + s * 2048 + 512);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            half8 kh, kl;
+            split8(kb[s % KP][0], kb[s % KP][1], kh, kl);
+            if (s + KP < 8) {
+                kb[s % KP][0] = *(const f32x4*)(Ks + kaddr + (s + KP) * 2048);
+                kb[s % KP][1] = *(const f32x4*)(Ks + kaddr + (s + KP) * 2048 + 512);
+            }
+            Sh = mfma32(kh, qh[s], Sh);
+            Sl = mfma32(kh, ql[s], Sl);
+            Sl = mfma32(kl, qh[s], Sl);
+        }
+        f32x16 S = Sh + Sl;
+#pragma unroll
+        for (int a = 0; a < 4; a++) xs[w][a][lane] = f32x4{S[4 * a], S[4 * a + 1], S[4 * a + 2], S[4 * a + 3]};
+        lds_barrier();
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const f32x4 o = xs[w ^ 1][a][lane];
+#pragma unroll
+            for (int b = 0; b < 4; b++) S[4 * a + b] += o[b];  // a + b == b + a: both waves hold the same S
+        }
+        // register i of lane (r, h) is key 8h + i (i < 8) or 16 + 8h + i - 8 of the tile for row r
+        if (!__all(k0 >= start && k0 + 32 <= vis)) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int key = k0 + 8 * h + i + (i >= 8 ? 8 : 0);
+                S[i] = (key >= start && key < vis) ? S[i] : NEG_INF;
+            }
+        }
+        float mt = S[0];
+#pragma unroll
+        for (int i = 1; i < 16; i++) mt = fmaxf(mt, S[i]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        mt *= scale2;  // scale2 > 0
+        const bool rescale = m != NEG_INF && mt > m + LAZY2;
+        const float mr = m == NEG_INF || rescale ? fmaxf(m, mt) : m;
+        float cf = 1.f;
+        if (__any(rescale)) {  // register i of O holds row 8(i/4) + 4h + i%4, whose factor that row's lanes hold
+            cf = rescale ? fast_exp2(m - mr) : 1.f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float f = __shfl(cf, 8 * (i >> 2) + 4 * h + (i & 3));
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++) O[nb][i] *= f;
+            }
+        }
+        m = mr;
+        const float base = mr == NEG_INF ? 0.f : mr;
+        float p[16], ls = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            p[i] = fast_exp2(__builtin_fmaf(S[i], scale2, -base));
+            ls += p[i];
+        }
+        lsum = lsum * cf + ls;
+        half8 ph[2], pl[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            split8(f32x4{p[8 * k], p[8 * k + 1], p[8 * k + 2], p[8 * k + 3]},
+                   f32x4{p[8 * k + 4], p[8 * k + 5], p[8 * k + 6], p[8 * k + 7]}, ph[k], pl[k]);
+        // key step k: keys 16k + 8h .. +7 = V groups 4k + 2h, +1; dim block nb: dims 128dh + 32nb + r
+        auto vaddr = [&](int i) { return Vs + ((4 * (i >> 2) + 2 * h) * HD + 128 * dh + 32 * (i & 3) + r) * 16; };
+        constexpr int VP = 2;
+        f32x4 vb[VP][2];
+#pragma unroll
+        for (int i = 0; i < VP; i++) {
+            vb[i][0] = *(const f32x4*)vaddr(i);
+            vb[i][1] = *(const f32x4*)(vaddr(i) + HD * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            half8 vh, vl;
+            split8(vb[i % VP][0], vb[i % VP][1], vh, vl);
+            if (i + VP < 8) {
+                vb[i % VP][0] = *(const f32x4*)vaddr(i + VP);
+                vb[i % VP][1] = *(const f32x4*)(vaddr(i + VP) + HD * 16);
+            }
+            O[i & 3] = mfma32(pl[i >> 2], vh, mfma32(ph[i >> 2], vl, mfma32(ph[i >> 2], vh, O[i & 3])));
+        }
+    }
+
+    // partials of this wave's rows of present tokens: its 128 dims; m and l from the dim-half-0 wave
+    lsum += __shfl_xor(lsum, 32);
+    const size_t rpk = (size_t)T * GQA;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int ri = 8 * (i >> 2) + 4 * h + (i & 3);
+        if (t0 + (ri >> 3) < T) {
+            float* pp = part + ((kvh * rpk + (size_t)t0 * GQA + ri) * nch + sp) * PART + PACC + 128 * dh + r;
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++) pp[32 * nb] = O[nb][i];
+        }
+    }
+    if (dh == 0 && h == 0 && tr < T) {
+        float* pp = part + ((kvh * rpk + (size_t)t0 * GQA + r) * nch + sp) * PART;
+        pp[0] = m;
+        pp[1] = lsum;
+    }
+}
+
 }  // namespace
 
 PrefillPlan prefill_plan(int T, int n) {
@@ -273,6 +463,16 @@ PrefillPlan prefill_plan(int T, int n) {
     const int blocks = 2 * ((T + PT - 1) / PT);  // work-groups per split
     int nch = 256 * WGS_PER_CU / blocks;         // about WGS_PER_CU work-groups per CU
     const int most = kend / 64;                  // splits of at least 64 positions
+    nch = nch > most ? most : nch;
+    nch = nch < 1 ? 1 : nch > 16 ? 16 : nch;
+    return PrefillPlan{kend, nch};
+}
+
+PrefillPlan prefill32_plan(int T, int n) {
+    const int kend = n + T - 1;
+    const int blocks = KVH * ((T + P32_PT - 1) / P32_PT);  // work-groups per split
+    int nch = 256 / blocks;                               // about one work-group per CU
+    const int most = kend / 64;                           // splits of at least 64 positions
     nch = nch > most ? most : nch;
     nch = nch < 1 ? 1 : nch > 16 ? 16 : nch;
     return PrefillPlan{kend, nch};
@@ -289,6 +489,17 @@ hipError_t launch_prefill(const Geom& g, const void* base, int layer, const floa
     dim3 grid((T + PT - 1) / PT * p.nch * KVH);
     return launch(prefill_f16, grid, dim3(NW * 64), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
                   p.nch, ws);
+}
+
+hipError_t launch_prefill_f32(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
+                              float scale, const PrefillPlan& p, float* ws, const Launch& L) {
+    if (g.fmt != 1) return hipErrorNotSupported;
+    const char* b = (const char*)base;
+    const float* kp = (const float*)(b + g.plane(layer, 0, 0) * g.plane_bytes());
+    const float* vp = (const float*)(b + g.plane(layer, 1, 0) * g.plane_bytes());
+    dim3 grid((T + P32_PT - 1) / P32_PT * p.nch * KVH);
+    return launch(prefill_f32, grid, dim3(P32_NW * 64), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E,
+                  p.span, p.nch, ws);
 }
 
 }  // namespace mkv

@@ -313,13 +313,13 @@ int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, fl
                 return launch_merge(h->pws, T * GQA, T, n, start, p.span, p.nch, gate, out, L);
             });
     } else {
-        // f32 store: the fp32 matrix-core kernel over blocks of 4 tokens, each token's causal window
-        const Attn32Plan p = attn32_plan(T, n, start);
+        // f32 store: 16-token work-groups over an LDS ring, f32-class arithmetic
+        const PrefillPlan p = prefill32_plan(T, n);
         const size_t need = prefill_ws_floats(T, p.nch);
         if (!prefill_ws(h, need, e))
             return fail(MKV_E_NOMEM, "mkv_prefill: %zu bytes of split-K partials", need * sizeof(float));
         e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
-            return launch_attn_f32(h->g, h->base, layer, q, T, n, start, scale, p, T * GQA, h->pws, FusedAppend{}, L);
+            return launch_prefill_f32(h->g, h->base, layer, q, T, n, start, scale, p, h->pws, L);
         });
         if (e == hipSuccess)
             e = traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {

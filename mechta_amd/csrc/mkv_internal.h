@@ -157,9 +157,9 @@ hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, 
 // q/k producer (rmsnorm of the q and k heads, rope2 of q) of ntok tokens; tab: [ntok][64] device RoPE rows.
 hipError_t launch_qk_produce(int ntok, const float* qf, const float* kb, const float* q_w, const float* k_w,
                              float eps, const float* tab, float* q_out, float* kn_out, const Launch& L);
-// Attention over the f32 store (kv_attn32.hip), decode (T <= 4) and prefill alike: nrb blocks of 4 tokens, splits
-// [c0, nch) of [0, span) (chunk_lo), or for decode (span 0) nch work-groups per kv head taking the window's 32-key
-// tiles round robin; partials [kvh][row < rpk][nch][PART], then launch_merge.
+// Decode attention over the f32 store (kv_attn32.hip, T <= 4): one block of 4 tokens (nrb = 1, c0 = 0), nch
+// work-groups per kv head taking the window's 32-key tiles round robin (span 0); partials [kvh][row < rpk][nch][PART],
+// then launch_merge.
 struct Attn32Plan {
     int span, nch, c0, nrb;
 };
@@ -167,7 +167,7 @@ Attn32Plan attn32_plan(int T, int n, int start);
 hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
                            float scale, const Attn32Plan& p, int rpk, float* part, const FusedAppend& fa,
                            const Launch& L);
-// Prefill (f16 store): split-K pass into the partials ws, then launch_merge with the returned plan.
+// Prefill: split-K pass into the partials ws, then launch_merge with the returned plan.
 struct PrefillPlan {
     int span, nch;  // splits of [0, span) as chunk_lo
 };
@@ -175,5 +175,9 @@ PrefillPlan prefill_plan(int T, int n);
 size_t prefill_ws_floats(int T, int nch);
 hipError_t launch_prefill(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
                           float scale, const PrefillPlan& p, float* ws, const Launch& L);
+// f32 store: prefill_f32 (16-token work-groups over an LDS ring, f32-class arithmetic)
+PrefillPlan prefill32_plan(int T, int n);
+hipError_t launch_prefill_f32(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
+                              float scale, const PrefillPlan& p, float* ws, const Launch& L);
 
 }  // namespace mkv
