@@ -316,7 +316,8 @@ def bench_cfg4(torch, mk, positions):
 def bench_cfg5(torch, mk, reps=3):
     """f32 store, 10 layers x 16,384 positions (671 MB): snapshot to pinned host memory, restore
     into a fresh store, then a 4-token verify per layer, checked bit-identical to the same verify before the
-    snapshot. Returns the snapshot and restore rates (host link), the verify's µs per layer and the identity flag."""
+    snapshot. Returns the snapshot and restore rates (host link), the verify's µs per layer, the identity flag, and
+    a 512-token prefill on the restored store (prefill_f32 + merge, layers rotated)."""
     L, N0, NT = 10, 16384, 4
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2032)
@@ -365,10 +366,24 @@ def bench_cfg5(torch, mk, reps=3):
         verify(b)
     e1.record()
     torch.cuda.synchronize()
+    verify_us = e0.elapsed_time(e1) / (10 * L) * 1000
+    # the f32 store's prefill (prefill_f32 + merge): a 512-token block ending at the restored length, layers rotated
+    q512 = seeded_normal(torch, gen, (512, 16, 256)) / 16
+    n512 = p - 511
+    for layer in range(3):
+        b.prefill(layer, q512, n512, scale=1.0)
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(10):
+        b.prefill(i % L, q512, n512, scale=1.0)
+    e1.record()
+    torch.cuda.synchronize()
+    pf_ms = e0.elapsed_time(e1) / 10
+    flops = 4 * 256 * 16 * sum(n512 + t for t in range(512))
     b.close()
     return dict(snapshot_gbps=round(nb / t_snap / 1e9, 2), restore_gbps=round(nb / t_rest / 1e9, 2),
-                snapshot_mb=round(nb / 1e6, 1), verify_us_per_layer=round(e0.elapsed_time(e1) / (10 * L) * 1000, 2),
-                bit_identical=bool(same))
+                snapshot_mb=round(nb / 1e6, 1), verify_us_per_layer=round(verify_us, 2), bit_identical=bool(same),
+                f32_prefill_512_ms=round(pf_ms, 3), f32_prefill_tflops=round(flops / (pf_ms * 1e-3) / 1e12, 1))
 
 
 def bench_flint(torch, mk, ctx=32768):
