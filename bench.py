@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--counter-summary", metavar="PMC_DIR",
                     help="no GPU work: mean of every counter per kernel and grid of a rocprofv3 --pmc output directory, "
                          "as a markdown table")
+    ap.add_argument("--probe-sweep", action="store_true",
+                    help="only the plain-read probe over launch shapes (work-groups, threads, loads in flight, load "
+                         "policy, stage order, a tail write), as a markdown table")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="no GPU work: group a rocprofv3 --kernel-trace csv by kernel and grid (launches, mean, median, "
                          "min, max microseconds) as a markdown table")
@@ -458,6 +461,74 @@ def bench_read_floor(torch, nbytes, nbuf=10, reps=60):
             "what": "one launch of a plain streaming read of the decode launch's K+V bytes (libmkv_probe.so)"}
 
 
+def probe_sweep(torch, nbytes=134348800, nbuf=10, reps=60):
+    """The plain-read probe (libmkv_probe.so) over launch shapes, for the bytes of one cfg2 decode launch, over nbuf
+    buffers in turn (nothing from the last-level cache). Prints a markdown table: per shape the launch duration from
+    the dispatch timestamps (mean, best) and the time per launch back to back."""
+    import ctypes
+    here = os.path.dirname(os.path.abspath(__file__))
+    probe = ctypes.CDLL(os.path.join(here, "mechta_amd", "lib", "libmkv_probe.so"))
+    unit = 1024 * 128
+    nbytes = (nbytes + unit - 1) // unit * unit
+    bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(nbuf)]
+    torch.cuda.synchronize()
+    ptrs = (ctypes.c_void_p * nbuf)(*[b.data_ptr() for b in bufs])
+    # (what, work-groups, threads, depth, non-temporal, round robin, tail bytes (+ store policy 0..3), bytes)
+    shapes = [("empty launch", 248, 512, 2, 1, 1, 0, 0),
+              ("default: 248 x 512, 2 stages in flight, nt, round robin", 248, 512, 2, 1, 1, 0, nbytes)]
+    shapes += [(f"depth {d}", 248, 512, d, 1, 1, 0, nbytes) for d in (1, 3, 4)]
+    shapes += [(f"{w} work-groups", w, 512, 2, 1, 1, 0, nbytes) for w in (124, 186, 256, 496, 512, 1024, 2048)]
+    shapes += [("124 work-groups, depth 3", 124, 512, 3, 1, 1, 0, nbytes),
+               ("124 x 1024 threads", 124, 1024, 2, 1, 1, 0, nbytes)]
+    shapes += [(f"{w} x 256 threads", w, 256, 2, 1, 1, 0, nbytes) for w in (248, 496, 992)]
+    shapes += [(f"{w} x 256 threads, depth 4", w, 256, 4, 1, 1, 0, nbytes) for w in (496, 992)]
+    shapes += [("248 x 1024 threads", 248, 1024, 2, 1, 1, 0, nbytes),
+               ("default load policy", 248, 512, 2, 0, 1, 0, nbytes),
+               ("contiguous range per work-group", 248, 512, 2, 1, 0, 0, nbytes),
+               ("tail write 33 KB per work-group", 248, 512, 2, 1, 1, 33280, nbytes),
+               ("tail write 16 KB per work-group", 248, 512, 2, 1, 1, 16640, nbytes),
+               ("tail write 33 KB, sc1 stores", 248, 512, 2, 1, 1, 33280 + 1, nbytes),
+               ("tail write 33 KB, nt stores", 248, 512, 2, 1, 1, 33280 + 2, nbytes),
+               ("tail write 33 KB, sc0 sc1 stores", 248, 512, 2, 1, 1, 33280 + 3, nbytes),
+               ("fused merge: partials 33 KB + barrier per half (wait 1) + merge read", 248, 512, -4, 1, 1, 0, nbytes),
+               ("fused merge, wait 20", 248, 512, -5, 1, 1, 0, nbytes),
+               ("fused merge: partials only", 248, 512, -1, 1, 1, 0, nbytes),
+               ("fused merge: partials + fence + merge read, no counters", 248, 512, -2, 1, 1, 0, nbytes),
+               ("fused merge: partials + fence + arrival atomic + merge read", 248, 512, -3, 1, 1, 0, nbytes),
+               ("fused merge, sc1 partials, relaxed counters (wait 1)", 248, 512, -6, 1, 1, 0, nbytes),
+               ("fused merge, sc1 partials, relaxed counters (wait 8)", 248, 512, -7, 1, 1, 0, nbytes),
+               ("fused merge, sc1 partials, arrivals only (no wait)", 248, 512, -8, 1, 1, 0, nbytes),
+               ("fused merge, sc1 partials, 8 sub-counters + top", 248, 512, -9, 1, 1, 0, nbytes),
+               ("fused merge, sc1 partials, a flag per work-group (epoch)", 248, 512, -10, 1, 1, 0, nbytes),
+               ("empty launch, sc1 fused-merge tail only", 248, 512, -6, 1, 1, 0, 0),
+               ("empty launch, sc1 tail, 8 sub-counters", 248, 512, -9, 1, 1, 0, 0),
+               ("empty launch, sc1 tail, flags", 248, 512, -10, 1, 1, 0, 0),
+               ("half the bytes (67 MB)", 248, 512, 2, 1, 1, 0, nbytes // 2 // unit * unit),
+               ("4x the bytes (537 MB, cfg4 per layer)", 248, 512, 2, 1, 1, 0, None)]
+    rows = []
+    for what, wgs, thr, depth, nt, rr, tail, nb in shapes:
+        if nb is None:  # 4x: the buffers hold it only in pairs of 4 consecutive tensors; use one big buffer set
+            big = [torch.ones(nbytes, dtype=torch.float32, device="cuda") for _ in range(3)]
+            p = (ctypes.c_void_p * 3)(*[b.data_ptr() for b in big])
+            nb, pp, nn = nbytes * 4, p, 3
+        else:
+            big, pp, nn = None, ptrs, nbuf
+        mean, best, wall = ctypes.c_float(), ctypes.c_float(), ctypes.c_float()
+        rc = probe.mkv_probe_run(pp, nn, ctypes.c_size_t(nb), wgs, thr, depth, nt, rr, ctypes.c_size_t(tail), reps,
+                                 ctypes.byref(mean), ctypes.byref(best), ctypes.byref(wall))
+        if rc != 0:
+            raise RuntimeError(f"mkv_probe_run failed on {what}: HIP error {rc}")
+        del big
+        gbs = nb / (mean.value * 1e-6) / 1e9 if nb else 0.0
+        rows.append((what, wgs, thr, depth, nb, mean.value, best.value, wall.value, gbs))
+        print(f"# {what}: {mean.value:.2f} us", file=sys.stderr, flush=True)
+    print("| shape | work-groups | threads | stages in flight | MB | mean us | best us | back-to-back us | GB/s (mean) |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for what, wgs, thr, depth, nb, mean, best, wall, gbs in rows:
+        print(f"| {what} | {wgs} | {thr} | {depth} | {nb / 1e6:.1f} | {mean:.2f} | {best:.2f} | {wall:.2f} | "
+              f"{gbs:.0f} |")
+
+
 def cpu_baseline(dec, budget_s):
     """The oracle's attn_dmx + append on the bench's own cache, on this host's cores."""
     import numpy as np
@@ -502,6 +573,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU", file=sys.stderr)
         sys.exit(1)
+    if args.probe_sweep:
+        probe_sweep(torch)
+        return
     dec = bench_decode(torch, mk, args.steps, args.warmup)
     ms_step = dec["ms"] / dec["steps"]
     bytes_rw = dec["kend"] * 2 * 256 * 2 * 2 + 4 * 2 * 256 * 2 * 2

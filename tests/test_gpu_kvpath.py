@@ -175,6 +175,23 @@ def test_decode_f16(torch_gpu, mk, ctx, n0, ntok, start):
         assert_attn_close(out, O.attn_fd(F16, kc, vc, q, n0, start=start), what="vs attn_fd")
 
 
+def test_decode_split_count_sequence(torch_gpu, mk):
+    """A sequence of decodes on one store whose split counts repeat and alternate (124, 79, 124, 79 with one token,
+    47, 124, 79, 124 with one token, 124): every output against the oracle (the workspace is shared by all of them)."""
+    torch = torch_gpu
+    with mk.KvStore(1, 12288, F16) as st:
+        fill(torch, st, 0, F16, 10000, seed=77)
+        kc, vc = caches_np(st, 0, 10000)
+        for i, (n0, ntok) in enumerate([(9000, 4), (5000, 4), (9000, 4), (5000, 1), (3000, 4), (9000, 4), (5000, 4),
+                                        (9000, 1), (9000, 4)]):
+            print(f"split count sequence step {i}: n0={n0} ntok={ntok}", flush=True)
+            q = q_inputs(500 + i, ntok)
+            out = st.decode(0, dev(torch, q), n0).cpu().numpy()
+            ref = O.attn_dmx(kc, vc, q, n0) if ntok > 1 else O.attn_fd(F16, kc, vc, q, n0)
+            assert np.isfinite(out).all(), f"step {i}: non-finite output"
+            assert_attn_close(out, ref, what=f"step {i}")
+
+
 @pytest.mark.parametrize("ctx,n0,ntok,start", [(4096, 300, 4, 0), (4096, 1000, 1, 0), (8192, 5000, 4, 17),
                                                (4096, 2, 1, 0), (4096, 129, 2, 0), (20480, 19000, 3, 0),
                                                (20480, 19001, 4, 12345), (8192, 40, 4, 33)])
