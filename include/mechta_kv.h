@@ -64,6 +64,17 @@ typedef struct mkv_store mkv_t;
 #define MKV_HEAD_DIM 256
 #define MKV_PREFILL_MAX 512 /* tokens per prefill block, NB (engine.rs:18) */
 
+/* Bytes of one K or V cache of one layer for ctx positions: ctx x 512 elements of the format, as the reference's
+ * KvFormat::buffer_bytes_for (engine.rs:64-65); 0 for a bad format. */
+size_t mkv_buffer_bytes(int ctx, int fmt);
+/* Device bytes mkv_create(layers, ctx, fmt) allocates: the planes (exactly 2 x layers x mkv_buffer_bytes(ctx, fmt):
+ * the blocked layout holds ctx x 512 elements per layer and K|V with no padding, ctx being a multiple of 1024), 64 KiB
+ * of slack past the last plane, the decode partials (2 kv heads x 32 rows x min(ctx / 64 + 2, 256) splits x 1,040
+ * bytes) and the prefill partials (68,157,440 bytes: 2 kv heads x 4,096 (token, split) pairs x 8 heads x 1,040
+ * bytes). 0 for arguments mkv_create refuses. The reference's memory check sizes the same cache as
+ * 2 x layers x buffer_bytes_for(ctx) (memcheck.rs:110-111). */
+size_t mkv_store_bytes(int layers, int ctx, int fmt);
+
 /* Allocates the store: layers x {K, V} x 2 heads x ctx x 256 elements, zero filled, and the split-K workspaces.
  * Replaces the per-layer KV buffer allocation (engine.rs:493-496) with the ctx check of check_ctx (engine.rs:28-33).
  * stream: a hipStream_t (NULL = the default stream). */

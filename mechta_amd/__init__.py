@@ -24,7 +24,7 @@ SYMBOLS = ["mkv_create", "mkv_destroy", "mkv_set_stream", "mkv_sync", "mkv_last_
            "mkv_append", "mkv_set_len", "mkv_decode", "mkv_append_decode", "mkv_prefill", "mkv_snapshot_bytes",
            "mkv_snapshot", "mkv_restore", "mkv_read_rows", "mkv_write_rows", "mkv_trace", "mkv_trace_read",
            "mkv_rope_table", "mkv_root_key", "mkv_root_save", "mkv_root_wait", "mkv_root_info", "mkv_root_load",
-           "mkv_rope_table_dev", "mkv_qk_norm_rope"]
+           "mkv_rope_table_dev", "mkv_qk_norm_rope", "mkv_buffer_bytes", "mkv_store_bytes"]
 SPAN_KV_WRITE, SPAN_CORE, SPAN_MERGE = 0, 1, 2
 
 
@@ -75,6 +75,8 @@ def lib():
             "mkv_root_load": ([P, ctypes.c_char_p, P, P, P], I),
             "mkv_rope_table_dev": ([P, I, ctypes.POINTER(P)], I),
             "mkv_qk_norm_rope": ([P, I, I, P, P, P, P, F, P, P], I),
+            "mkv_buffer_bytes": ([I, I], S),
+            "mkv_store_bytes": ([I, I, I], S),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -82,6 +84,16 @@ def lib():
             f.restype = res
         _lib = L
     return _lib
+
+
+def buffer_bytes(ctx, fmt):
+    """Bytes of one K or V cache of one layer (the reference's KvFormat::buffer_bytes_for)."""
+    return lib().mkv_buffer_bytes(ctx, fmt)
+
+
+def store_bytes(layers, ctx, fmt):
+    """Device bytes mkv_create allocates for such a store (0 if it would refuse the arguments)."""
+    return lib().mkv_store_bytes(layers, ctx, fmt)
 
 
 def _check(rc):
@@ -147,6 +159,11 @@ def _ptr_array(arrays):
     return (ctypes.c_void_p * max(len(arrays), 1))(*[a.ctypes.data for a in arrays])
 
 
+def _pinned(t, who):
+    if t.device.type != "cpu" or not t.is_pinned():
+        raise ValueError(f"{who}: the host buffer must be pinned host memory (torch pin_memory=True / hipHostMalloc)")
+
+
 class KvStore:
     """The KV store of `layers` full-attention layers (K and V, 2 KV heads x 256, `ctx` positions, f16 or f32).
 
@@ -187,6 +204,7 @@ class KvStore:
 
     def sync(self):
         _check(lib().mkv_sync(self._h))
+        self._restore_src = None  # the copy out of it has landed
 
     def length(self, layer=0):
         n = ctypes.c_int()
@@ -251,11 +269,16 @@ class KvStore:
         nb = self.snapshot_bytes(p)
         if host is None:
             host = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+        _pinned(host, "snapshot")
         _check(lib().mkv_snapshot(self._h, p, _ptr(host), host.numel() * host.element_size()))
         return host
 
     def restore(self, p, host):
+        """Positions [0, p) of every layer from a snapshot in pinned host memory. The copy is only enqueued: the
+        store keeps a reference to `host` until the next sync() (do not write into it before then)."""
+        _pinned(host, "restore")
         _check(lib().mkv_restore(self._h, p, _ptr(host), host.numel() * host.element_size()))
+        self._restore_src = host
 
     def read_rows(self, layer, which, p0, p1, out=None):
         """Positions [p0, p1) of K or V in the reference layout [pos][2][256] (int16 bit patterns for f16)."""

@@ -53,11 +53,15 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
                                                   int start, float scale2, int s0, int nu,
                                                   float* __restrict__ part, const float* __restrict__ akn,
                                                   const float* __restrict__ av, const float* __restrict__ atab,
-                                                  int apos, int antok) {
+                                                  int apos, int antok, int rpk) {
     const int kvh = blockIdx.y, c = blockIdx.x, nch = gridDim.x, tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int h = lane >> 5, r = lane & 31, l16 = lane & 15, g4 = lane >> 4;
+    // the call's keys end where its last token's do; blockIdx.z = block of 4 tokens (a small prefill block runs one
+    // per work-group column, with the same stages), whose token 0 sees [start, nb)
     const int kend = n + ntok - 1;
+    const int zb = blockIdx.z, nb = n + 4 * zb, ntb = min(4, ntok - 4 * zb);
+    q += (size_t)4 * zb * QH * HD;
     // Stages are dealt so that the partial round comes first: with R = nu / nch and r = nu % nch, stage u >= r goes
     // to work-group (u - r) % nch, so every work-group takes R of them and the last stage (the one holding appended
     // rows) goes to work-group nch - 1. The first r stages are the partial round: when 2r <= nch they are split into
@@ -145,7 +149,7 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int idx = tid + 512 * i, row = idx >> 5, d8 = (idx & 31) * 8, tq = row >> 3;
-        const float* qr = q + ((size_t)min(tq, ntok - 1) * QH + kvh * GQA + (row & 7)) * HD + d8;
+        const float* qr = q + ((size_t)min(tq, ntb - 1) * QH + kvh * GQA + (row & 7)) * HD + d8;
         xq[i][0] = *(const float4*)qr;
         xq[i][1] = *(const float4*)(qr + 4);
     }
@@ -170,7 +174,7 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     for (int i = 0; i < 2; i++) {
         const int idx = tid + 512 * i, row = idx >> 5, d8 = (idx & 31) * 8, tq = row >> 3;
         float4 x0 = xq[i][0], x1 = xq[i][1];
-        if (tq >= ntok) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tq >= ntb) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (EXACT) {
             half8 hi, lo;
             split8(f32x4{x0.x, x0.y, x0.z, x0.w}, f32x4{x1.x, x1.y, x1.z, x1.w}, hi, lo);
@@ -185,7 +189,7 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
 
     // softmax role: thread (srow, sq) owns keys 4sq .. 4sq+3 of row srow; the row's 16 threads keep identical m, l
     const int srow = tid >> 4, sq = tid & 15;
-    const int vis = min(n + (srow >> 3), kend);  // row srow sees keys < vis (rows of absent tokens: < kend)
+    const int vis = min(nb + (srow >> 3), kend);  // row srow sees keys < vis (rows of absent tokens: < kend)
     float m_run = NEG_INF, l_run = 0.f;
     f32x16 O = f32x16{};
 
@@ -228,7 +232,7 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
         const float4 x1 = *(const float4*)&ss[buf][1][srow][4 * sq];
         float sv[4] = {(x0.x + x1.x) * scale2, (x0.y + x1.y) * scale2, (x0.z + x1.z) * scale2, (x0.w + x1.w) * scale2};
         const int kcap = k0 + klen(j);
-        if (!(k0 >= start && kcap <= n && kcap == k0 + KPS)) {  // the stage crosses a row's window or is a half
+        if (!(k0 >= start && kcap <= nb && kcap == k0 + KPS)) {  // the stage crosses a row's window or is a half
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int key = k0 + 4 * sq + i;
@@ -364,14 +368,15 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     }
 
     // partials: this wave's 32 dims of every row of a present token; m and l from the rows' softmax threads
-    const int nrows = 8 * ntok;
+    const int nrows = 8 * ntb;
+    const int rz = kvh * rpk + 32 * zb;  // partial row of this block's row 0
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         const int ri = 8 * (i >> 2) + 4 * h + (i & 3);
-        if (ri < nrows) part[((size_t)(kvh * ROWS + ri) * nch + c) * PART + PACC + 32 * w + r] = O[i];
+        if (ri < nrows) part[((size_t)(rz + ri) * nch + c) * PART + PACC + 32 * w + r] = O[i];
     }
     if (sq == 0 && srow < nrows) {
-        float* p = part + ((size_t)(kvh * ROWS + srow) * nch + c) * PART;
+        float* p = part + ((size_t)(rz + srow) * nch + c) * PART;
         p[0] = m_run;
         p[1] = l_run;
     }
@@ -524,10 +529,34 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
     void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
     void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
     const float scale2 = scale * LOG2E;
-    if (g.fmt != 0) return hipErrorNotSupported;
+    if (g.fmt != 0 || ntok > 4) return hipErrorNotSupported;
     return launch(ntok == 1 || start > 0 ? decode_f16<true> : decode_f16<false>, dim3(p.nch, KVH), dim3(512), L, kp, vp,
                   g.plane_elems, q, ntok, n, start, scale2,
-                  p.s0, p.nu, ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
+                  p.s0, p.nu, ws.part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok, ROWS);
+}
+
+SmallPlan small_prefill_plan(int T, int n, int start) {
+    // the decode's stages over the whole block's keys; at most DEC_WG work-groups per (kv head, 4-token block) and
+    // about DEC_WG in all per kv head once there are several blocks (each block streams every stage)
+    const int nzb = (T + 3) / 4;
+    DecodePlan d = decode_plan(n, T, start);
+    const int cap = max(8, DEC_WG / nzb);
+    d.nch = min(d.nch, cap);
+    return SmallPlan{d, nzb};
+}
+
+size_t small_prefill_ws_floats(int T, int nch) { return (size_t)KVH * 32 * ((T + 3) / 4) * nch * PART; }
+
+hipError_t launch_small_prefill(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
+                                float scale, const SmallPlan& p, float* ws, const Launch& L) {
+    if (g.fmt != 0 || T < 1 || T > SMALL_PREFILL_MAX) return hipErrorNotSupported;
+    char* b = (char*)base;
+    void* kp = b + g.plane(layer, 0, 0) * g.plane_bytes();
+    void* vp = b + g.plane(layer, 1, 0) * g.plane_bytes();
+    const float scale2 = scale * LOG2E;
+    return launch(decode_f16<true>, dim3(p.d.nch, KVH, p.nzb), dim3(512), L, kp, vp, g.plane_elems, q, T, n, start,
+                  scale2, p.d.s0, p.d.nu, ws, (const float*)nullptr, (const float*)nullptr, (const float*)nullptr, 0, 0,
+                  32 * p.nzb);
 }
 
 hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,

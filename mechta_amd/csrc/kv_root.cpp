@@ -9,6 +9,7 @@
 // The store keeps its own tiled layout; read_rows / write_rows (kv_append.hip) convert on the device.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -110,10 +111,36 @@ int scan(const char* path, RootInfo& ri) {
 namespace mkv {
 void root_join(mkv_store* h) {
     if (h->root_thread.joinable()) h->root_thread.join();
-    if (h->root_host) {
-        (void)hipHostFree(h->root_host);
+}
+
+void root_free(mkv_store* h) {
+    root_join(h);
+    if (h->root_host) (void)hipHostFree(h->root_host);
+    h->root_host = nullptr;
+    h->root_cap = 0;
+}
+
+// The handle's pinned host buffer of at least `bytes` (kept for later calls, grown only when a larger one is needed);
+// the caller has joined the background write that may be reading it.
+char* root_pinned(mkv_store* h, size_t bytes) {
+    if (bytes <= h->root_cap) return (char*)h->root_host;
+    if (h->root_host) (void)hipHostFree(h->root_host);
+    h->root_host = nullptr;
+    h->root_cap = 0;
+    if (hipHostMalloc(&h->root_host, bytes, hipHostMallocDefault) != hipSuccess) {
         h->root_host = nullptr;
+        (void)hipGetLastError();
+        return nullptr;
     }
+    h->root_cap = bytes;
+    return (char*)h->root_host;
+}
+
+// Positions per run of the row conversion staged in the store's prefill workspace (device): the position-major words
+// of `run` positions of one plane pair fit it.
+int staging_run(const mkv_store* h) {
+    const size_t per_pos = (size_t)KVH * HD * h->g.bpe();
+    return (int)std::min<size_t>((size_t)h->g.ctx, h->pws_floats * sizeof(float) / per_pos);
 }
 }  // namespace mkv
 
@@ -146,9 +173,8 @@ int mkv_root_save(mkv_t* h, const char* path, int p, const uint32_t* tokens, int
     const uint64_t kw = kv_words_of(h->g.fmt, p);
     size_t total = HLEN + 24 + 4 * (size_t)p + (size_t)nk * 2 * (8 + 4 * kw);
     for (int i = 0; i < ns; i++) total += 16 + 4 * (ssm_words[i] + conv_words[i]);
-    char* buf = nullptr;
-    if (hipHostMalloc((void**)&buf, total, hipHostMallocDefault) != hipSuccess)
-        return fail(MKV_E_NOMEM, "mkv_root_save: %zu bytes of pinned host memory", total);
+    char* buf = root_pinned(h, total);
+    if (!buf) return fail(MKV_E_NOMEM, "mkv_root_save: %zu bytes of pinned host memory", total);
     size_t off = 0;
     auto put = [&](const void* src, size_t n) {
         if (n) memcpy(buf + off, src, n);
@@ -168,31 +194,28 @@ int mkv_root_save(mkv_t* h, const char* path, int p, const uint32_t* tokens, int
         put64(conv_words[i]);
         put(conv[i], 4 * conv_words[i]);
     }
-    // K and V words of every layer: converted to position-major on the device, then copied into the image
-    void* tmp = nullptr;
+    // K and V words of every layer: converted to position-major on the device, in runs of positions staged in the
+    // store's prefill workspace, then copied into the image
+    const int run = staging_run(h);
+    const size_t per_pos = (size_t)KVH * HD * h->g.bpe();
+    float* stage = h->pws;
     hipError_t e = hipSuccess;
-    if (kw && (e = hipMalloc(&tmp, 4 * kw)) != hipSuccess) {
-        (void)hipHostFree(buf);
-        return fail(MKV_E_NOMEM, "mkv_root_save: %llu bytes of device staging", (unsigned long long)(4 * kw));
-    }
     for (int l = 0; l < nk && e == hipSuccess; l++)
         for (int which = 0; which < 2 && e == hipSuccess; which++) {
             put64(kw);
-            if (kw) {
-                e = launch_read_rows(h->g, h->base, l, which, 0, p, tmp, Launch{h->stream});
-                if (e == hipSuccess) e = hipMemcpyAsync(buf + off, tmp, 4 * kw, hipMemcpyDeviceToHost, h->stream);
+            for (int p0 = 0; p0 < p && e == hipSuccess; p0 += run) {
+                const int p1 = std::min(p, p0 + run);
+                e = launch_read_rows(h->g, h->base, l, which, p0, p1, stage, Launch{h->stream});
+                if (e == hipSuccess)
+                    e = hipMemcpyAsync(buf + off + p0 * per_pos, stage, (p1 - p0) * per_pos, hipMemcpyDeviceToHost,
+                                       h->stream);
             }
             off += 4 * kw;
         }
     if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
-    if (tmp) (void)hipFree(tmp);
-    if (e != hipSuccess) {
-        (void)hipHostFree(buf);
-        return hip_fail(e, "mkv_root_save");
-    }
+    if (e != hipSuccess) return hip_fail(e, "mkv_root_save");
     const std::string file(path);
     if (background) {
-        h->root_host = buf;
         h->root_thread = std::thread([h, file, buf, total] {
             std::string err;
             h->root_rc = write_file(file, buf, total, err);
@@ -202,7 +225,6 @@ int mkv_root_save(mkv_t* h, const char* path, int p, const uint32_t* tokens, int
     }
     std::string err;
     const int rc = write_file(file, buf, total, err);
-    (void)hipHostFree(buf);
     return rc == MKV_OK ? MKV_OK : fail(rc, "%s", err.c_str());
 }
 
@@ -256,23 +278,27 @@ int mkv_root_load(mkv_t* h, const char* path, uint32_t* tokens, float* const* ss
     if (!ok) return fail(MKV_E_IO, "root file %s: read failed", path);
     const uint64_t kw = ri.kv_words;
     if (kw) {
-        // one vector at a time: file -> pinned host -> device staging -> store layout
-        char* host = nullptr;
-        void* tmp = nullptr;
-        if (hipHostMalloc((void**)&host, 4 * kw, hipHostMallocDefault) != hipSuccess)
-            return fail(MKV_E_NOMEM, "mkv_root_load: pinned host memory");
-        hipError_t e = hipMalloc(&tmp, 4 * kw);
+        // one vector at a time, in runs of positions: file -> the handle's pinned buffer -> the prefill workspace
+        // (device staging) -> store layout
+        const int run = staging_run(h);
+        const size_t per_pos = (size_t)KVH * HD * h->g.bpe();
+        char* host = root_pinned(h, (size_t)std::min(run, p) * per_pos);
+        if (!host) return fail(MKV_E_NOMEM, "mkv_root_load: pinned host memory");
+        hipError_t e = hipSuccess;
         for (int l = 0; l < h->g.layers && ok && e == hipSuccess; l++)
             for (int which = 0; which < 2 && ok && e == hipSuccess; which++) {
-                e = hipStreamSynchronize(h->stream);  // the previous vector left the pinned buffer
-                ok = e == hipSuccess && read_or_skip(nullptr, 8) && read_or_skip(host, 4 * kw);
-                if (!ok) break;
-                e = hipMemcpyAsync(tmp, host, 4 * kw, hipMemcpyHostToDevice, h->stream);
-                if (e == hipSuccess) e = launch_write_rows(h->g, h->base, l, which, 0, p, tmp, Launch{h->stream});
+                ok = read_or_skip(nullptr, 8);
+                for (int p0 = 0; p0 < p && ok && e == hipSuccess; p0 += run) {
+                    const int p1 = std::min(p, p0 + run);
+                    e = hipStreamSynchronize(h->stream);  // the previous run left the pinned buffer
+                    ok = e == hipSuccess && read_or_skip(host, (p1 - p0) * per_pos);
+                    if (!ok) break;
+                    e = hipMemcpyAsync(h->pws, host, (p1 - p0) * per_pos, hipMemcpyHostToDevice, h->stream);
+                    if (e == hipSuccess)
+                        e = launch_write_rows(h->g, h->base, l, which, p0, p1, h->pws, Launch{h->stream});
+                }
             }
         if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
-        if (tmp) (void)hipFree(tmp);
-        (void)hipHostFree(host);
         if (e != hipSuccess) return hip_fail(e, "mkv_root_load");
         if (!ok) return fail(MKV_E_IO, "root file %s: read failed (the store's positions [0, %d) are undefined)", path, p);
     }

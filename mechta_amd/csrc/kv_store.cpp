@@ -95,21 +95,18 @@ hipError_t decode_all(mkv_store* h, int layer, const float* q, int ntok, int n, 
                   [&](const Launch& L) { return launch_decode_merge(ntok, n, start, p, h->dws, gate, out, L); });
 }
 
-// Grows the prefill partials to `floats` (kept for later calls); false if the allocation fails.
-bool prefill_ws(mkv_store* h, size_t floats, hipError_t& e) {
-    if (floats <= h->pws_floats) return true;
-    e = hipStreamSynchronize(h->stream);
-    if (e == hipSuccess && h->pws) e = hipFree(h->pws);
-    h->pws = nullptr;
-    h->pws_floats = 0;
-    if (e == hipSuccess) e = hipMalloc(&h->pws, floats * sizeof(float));
-    if (e != hipSuccess) {
-        h->pws = nullptr;
-        (void)hipGetLastError();
-        return false;
+// Floats of the prefill partials workspace, allocated with the store: the largest any prefill plan uses (the f16
+// plans keep T * splits <= 4096, the f32 plan <= 2048, the small-block plan <= 4096 rows per kv head).
+size_t prefill_ws_max_floats() {
+    size_t m = 0;
+    for (int T = 1; T <= MKV_PREFILL_MAX; T++) {
+        for (int n : {1, 64, 1024, 8192, MKV_CTX_MAX - T}) {
+            m = std::max(m, prefill_ws_floats(T, prefill_plan(T, n).nch));
+            m = std::max(m, prefill_ws_floats(T, prefill32_plan(T, n).nch));
+            if (T <= SMALL_PREFILL_MAX) m = std::max(m, small_prefill_ws_floats(T, small_prefill_plan(T, n, 0).d.nch));
+        }
     }
-    h->pws_floats = floats;
-    return true;
+    return m;
 }
 
 void free_events(mkv_store* h) {
@@ -122,11 +119,42 @@ void free_events(mkv_store* h) {
     h->pool.clear();
 }
 
+// Device bytes of one store: the planes (layers x {K, V} x 2 heads x ctx x 256 elements: exactly the reference's
+// 2 x layers KV buffers of buffer_bytes_for(ctx), engine.rs:64-65) plus the slack past the last plane, then the decode
+// partials (2 kv heads x 32 rows x splits x 260 floats) and the prefill partials (prefill_ws_max_floats).
+struct StoreBytes {
+    size_t planes, slack, decode_ws, prefill_ws;
+    int max_chunks;
+    size_t total() const { return planes + slack + decode_ws + prefill_ws; }
+};
+StoreBytes store_bytes(int layers, int ctx, int fmt) {
+    StoreBytes b;
+    b.planes = (size_t)layers * 2 * KVH * (size_t)ctx * HD * (fmt == MKV_F16 ? 2 : 4);
+    b.slack = STORE_SLACK;
+    // decode splits: f16 one per 64-position stage, at most 124; f32 at most 248
+    b.max_chunks = std::min(ctx / 64 + 2, 256);
+    b.decode_ws = (size_t)KVH * ROWS * b.max_chunks * PART * sizeof(float);
+    b.prefill_ws = prefill_ws_max_floats() * sizeof(float);
+    return b;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* mkv_last_error(void) { return g_err; }
+
+size_t mkv_buffer_bytes(int ctx, int fmt) {
+    if (ctx < 0 || (fmt != MKV_F16 && fmt != MKV_F32)) return 0;
+    return (size_t)ctx * (KVH * HD) * (fmt == MKV_F16 ? 2 : 4);
+}
+
+size_t mkv_store_bytes(int layers, int ctx, int fmt) {
+    if (layers < 1 || layers > 4096 || (fmt != MKV_F16 && fmt != MKV_F32) || ctx % 1024 != 0 || ctx < MKV_CTX_MIN ||
+        ctx > MKV_CTX_MAX)
+        return 0;
+    return store_bytes(layers, ctx, fmt).total();
+}
 
 int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
     if (!out) return fail(MKV_E_ARG, "mkv_create: out is NULL");
@@ -146,22 +174,32 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
     h->len.assign(layers, 0);
     // + slack: a decode stage starting on a 32-position boundary reads up to 64 positions, which may reach past the
     // last plane's end (the rows read there are masked, never used)
-    size_t bytes = (size_t)layers * 2 * KVH * h->g.plane_bytes() + STORE_SLACK;
+    const StoreBytes sb = store_bytes(layers, ctx, fmt);
+    size_t bytes = sb.planes + sb.slack;
     hipError_t e = hipMalloc(&h->base, bytes);
     if (e != hipSuccess) {
         delete h;
         (void)hipGetLastError();
         return fail(MKV_E_NOMEM, "mkv_create: hipMalloc of %zu bytes failed", bytes);
     }
-    h->dws.max_chunks = std::min(ctx / 64 + 2, 256);  // decode splits: f16 one per 64-position stage, at most 124; f32 at most 248
-    size_t dws_bytes = (size_t)KVH * ROWS * h->dws.max_chunks * PART * sizeof(float);
-    e = hipMalloc(&h->dws.part, dws_bytes);
+    h->dws.max_chunks = sb.max_chunks;
+    e = hipMalloc(&h->dws.part, sb.decode_ws);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         (void)hipFree(h->base);
         if (h->dws.part) (void)hipFree(h->dws.part);
         delete h;
         return fail(MKV_E_NOMEM, "mkv_create: workspace allocation failed");
+    }
+    h->pws_floats = sb.prefill_ws / sizeof(float);
+    e = hipMalloc(&h->pws, h->pws_floats * sizeof(float));
+    if (e != hipSuccess) {
+        const size_t pbytes = h->pws_floats * sizeof(float);
+        (void)hipGetLastError();
+        (void)hipFree(h->base);
+        (void)hipFree(h->dws.part);
+        delete h;
+        return fail(MKV_E_NOMEM, "mkv_create: prefill workspace allocation (%zu bytes) failed", pbytes);
     }
     // zero fill: positions never written read as 0 (wgpu zero-initialises the reference's buffers)
     e = hipMemsetAsync(h->base, 0, bytes, h->stream);
@@ -180,7 +218,7 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
 
 int mkv_destroy(mkv_t* h) {
     if (!h) return MKV_OK;
-    root_join(h);
+    root_free(h);
     hipError_t e = hipStreamSynchronize(h->stream);
     free_events(h);
     (void)hipFree(h->base);
@@ -300,32 +338,32 @@ int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, fl
                 const float* gate) {
     if (int rc = check_attn(h, "mkv_prefill", layer, q, T, MKV_PREFILL_MAX, n, start, out)) return rc;
     hipError_t e = hipSuccess;
-    if (h->g.fmt == MKV_F16) {
-        const PrefillPlan p = prefill_plan(T, n);
-        const size_t need = prefill_ws_floats(T, p.nch);
-        if (!prefill_ws(h, need, e))
-            return fail(MKV_E_NOMEM, "mkv_prefill: %zu bytes of split-K partials", need * sizeof(float));
+    int span = 0, nch = 0, rpk = T * GQA;  // the split-K plan the merge reads
+    if (h->g.fmt == MKV_F16 && T <= SMALL_PREFILL_MAX) {
+        // blocks under 64 tokens: f32-class, as the reference's attn_fd4 (engine.rs:1237-1241)
+        const SmallPlan p = small_prefill_plan(T, n, start);
+        if (small_prefill_ws_floats(T, p.d.nch) > h->pws_floats) return fail(MKV_E_ARG, "mkv_prefill: workspace");
+        span = p.d.span;
+        nch = p.d.nch;
+        rpk = 32 * p.nzb;
         e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
-            return launch_prefill(h->g, h->base, layer, q, T, n, start, scale, p, h->pws, L);
+            return launch_small_prefill(h->g, h->base, layer, q, T, n, start, scale, p, h->pws, L);
         });
-        if (e == hipSuccess)
-            e = traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {
-                return launch_merge(h->pws, T * GQA, T, n, start, p.span, p.nch, gate, out, L);
-            });
     } else {
-        // f32 store: 16-token work-groups over an LDS ring, f32-class arithmetic
-        const PrefillPlan p = prefill32_plan(T, n);
-        const size_t need = prefill_ws_floats(T, p.nch);
-        if (!prefill_ws(h, need, e))
-            return fail(MKV_E_NOMEM, "mkv_prefill: %zu bytes of split-K partials", need * sizeof(float));
+        // f16: attn_fa_mx's arithmetic on 32-token work-groups; f32: 16-token work-groups, f32-class arithmetic
+        const bool f16 = h->g.fmt == MKV_F16;
+        const PrefillPlan p = f16 ? prefill_plan(T, n) : prefill32_plan(T, n);
+        if (prefill_ws_floats(T, p.nch) > h->pws_floats) return fail(MKV_E_ARG, "mkv_prefill: workspace");
+        span = p.span;
+        nch = p.nch;
         e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
-            return launch_prefill_f32(h->g, h->base, layer, q, T, n, start, scale, p, h->pws, L);
+            return f16 ? launch_prefill(h->g, h->base, layer, q, T, n, start, scale, p, h->pws, L)
+                       : launch_prefill_f32(h->g, h->base, layer, q, T, n, start, scale, p, h->pws, L);
         });
-        if (e == hipSuccess)
-            e = traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {
-                return launch_merge(h->pws, T * GQA, T, n, start, p.span, p.nch, gate, out, L);
-            });
     }
+    if (e == hipSuccess)
+        e = traced(h, MKV_SPAN_MERGE,
+                   [&](const Launch& L) { return launch_merge(h->pws, rpk, T, n, start, span, nch, gate, out, L); });
     return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_prefill");
 }
 

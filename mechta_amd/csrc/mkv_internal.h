@@ -150,6 +150,18 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
                               const Launch& L);
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
                                float* out, const Launch& L);
+// Small prefill blocks on the f16 store (T < SMALL_PREFILL_MAX): the reference runs them through attn_fd4 (f32 Q,
+// exact f32 softmax; engine.rs:1237-1241), so they run on decode_f16's f32-class arithmetic, one column of work-groups
+// per block of 4 tokens over the decode's stages; partials [kvh][row < 32 nzb][nch][PART], then launch_merge.
+constexpr int SMALL_PREFILL_MAX = 63;
+struct SmallPlan {
+    DecodePlan d;
+    int nzb;  // blocks of 4 tokens
+};
+SmallPlan small_prefill_plan(int T, int n, int start);
+size_t small_prefill_ws_floats(int T, int nch);
+hipError_t launch_small_prefill(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
+                                float scale, const SmallPlan& p, float* ws, const Launch& L);
 // Merge of split-K partials laid out [kvh][row < rpk][chunk < nch][PART], row = token*8 + head of the kv head:
 // out[t][head] for t < ntok over the chunks (chunk_lo of span, nch) holding a key of [start, n + t), optional gate.
 hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,

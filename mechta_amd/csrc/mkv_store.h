@@ -34,7 +34,8 @@ struct mkv_store {
     std::thread root_thread;
     int root_rc = 0;
     char root_err[512] = "";
-    void* root_host = nullptr;
+    void* root_host = nullptr;      // pinned host buffer of root saves and loads, reused (grown when too small)
+    size_t root_cap = 0;
 };
 
 
@@ -42,5 +43,6 @@ namespace mkv {
 extern thread_local char g_err[512];
 int fail(int code, const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
-void root_join(mkv_store* h);  // waits for a background root write, frees its host memory
+void root_join(mkv_store* h);  // waits for a background root write
+void root_free(mkv_store* h);  // joins, then frees the pinned root buffer
 }  // namespace mkv

@@ -443,6 +443,97 @@ void orc_attn_fa_f32(const float* kc, const float* vc, const float* q, int T, in
     fa_common(0, kc, vc, q, T, n, start, scale, 2048, sel, nsel, out);
 }
 
+/* ---------------------------------------------------------------- attn_fd4 ------------------------------------ */
+
+/* One (kvh, block of bl positions, token) unit of attn_fd4 (ops.wgsl:709-778) for the 8 heads of kvh: the block's
+ * positions in tiles of 64 (F4_B); scores are sums over the 64 vec4 groups of the row of dot(q4, k4) (each dot summed
+ * left to right), times scale, -3e38 for positions >= vis; per tile the exact running max mx = max(m, tile), the
+ * shrink cf = exp(m - mx) (0 while m is -3e38), w = exp(s - mx) (0 for masked scores), l = l * cf + sum w,
+ * acc = acc * cf + sum w * v. Partial [m, l, acc] per head. */
+static void fd4_unit(int fmt, const void* kc, const void* vc, const float* qt, int kvh, int b0, int bl, int vis,
+                     float scale, float* part_h0, size_t part_stride) {
+    float mm[8], ml[8], acc[8][ORC_D];
+    for (int h = 0; h < 8; h++) {
+        mm[h] = NEG_BIG;
+        ml[h] = 0.0f;
+        for (int d = 0; d < ORC_D; d++) acc[h][d] = 0.0f;
+    }
+    for (int t0 = b0; t0 < b0 + bl && t0 < vis; t0 += 64) {
+        float S[8][64];
+        for (int j = 0; j < 64; j++) {
+            const int key = t0 + j;
+            if (key >= vis) {
+                for (int h = 0; h < 8; h++) S[h][j] = NEG_BIG;
+                continue;
+            }
+            const size_t kb = (size_t)key * ORC_ROW + (size_t)kvh * ORC_D;
+            for (int h = 0; h < 8; h++) {
+                const float* q = qt + (size_t)(8 * kvh + h) * ORC_D;
+                float s = 0.0f;
+                for (int i = 0; i < 64; i++) {
+                    const float* q4 = q + 4 * i;
+                    float dt = q4[0] * kvget(fmt, kc, kb + 4 * i);
+                    dt += q4[1] * kvget(fmt, kc, kb + 4 * i + 1);
+                    dt += q4[2] * kvget(fmt, kc, kb + 4 * i + 2);
+                    dt += q4[3] * kvget(fmt, kc, kb + 4 * i + 3);
+                    s += dt;
+                }
+                S[h][j] = s * scale;
+            }
+        }
+        for (int h = 0; h < 8; h++) {
+            float mx = mm[h];
+            for (int j = 0; j < 64; j++) mx = fmaxf(mx, S[h][j]);
+            const float cf = mm[h] > -1.0e38f ? expf(mm[h] - mx) : 0.0f;
+            float sm = 0.0f;
+            for (int j = 0; j < 64; j++) {
+                const float v = S[h][j];
+                const float w = v > -1.0e38f ? expf(v - mx) : 0.0f;
+                S[h][j] = w;
+                sm += w;
+            }
+            mm[h] = mx;
+            ml[h] = ml[h] * cf + sm;
+            for (int d = 0; d < ORC_D; d++) acc[h][d] *= cf;
+        }
+        for (int j = 0; j < 64 && t0 + j < vis; j++) {
+            const size_t vb = (size_t)(t0 + j) * ORC_ROW + (size_t)kvh * ORC_D;
+            for (int d = 0; d < ORC_D; d++) {
+                const float vv = kvget(fmt, vc, vb + d);
+                for (int h = 0; h < 8; h++) acc[h][d] += S[h][j] * vv;
+            }
+        }
+    }
+    for (int h = 0; h < 8; h++) {
+        float* p = part_h0 + (size_t)h * part_stride;
+        p[0] = mm[h];
+        p[1] = ml[h];
+        for (int d = 0; d < ORC_D; d++) p[2 + d] = acc[h][d];
+    }
+}
+
+void orc_attn_fd4(int fmt, const void* kc, const void* vc, const float* q, int T, int n, float scale, int bl,
+                  float* out) {
+    const int nbmax = (n + T - 1 + bl - 1) / bl;
+    float* part = (float*)malloc(sizeof(float) * 258 * (size_t)T * ORC_H * (size_t)nbmax);
+    const int units = T * ORC_KVH * nbmax;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int u = 0; u < units; u++) {
+        const int t = u / (ORC_KVH * nbmax), kvh = (u / nbmax) % ORC_KVH, b = u % nbmax;
+        const int vis = n + t; /* token t sees [0, n + t) (extra = 0 in the prefill, engine.rs:920-921) */
+        if (b * bl >= vis) continue; /* not written; the merge takes the valid blocks only */
+        float* p = part + (((size_t)t * ORC_H + 8 * kvh) * nbmax + b) * 258;
+        fd4_unit(fmt, kc, vc, q + (size_t)t * ORC_H * ORC_D, kvh, b * bl, bl, vis, scale, p, (size_t)nbmax * 258);
+    }
+#pragma omp parallel for
+    for (int r = 0; r < T * ORC_H; r++) {
+        const int t = r / ORC_H;
+        const int nbv = (n + t + bl - 1) / bl; /* attn_fd_combine with flag = bl (ops.wgsl:527-528) */
+        combine(part + (size_t)r * nbmax * 258, nbv, out + (size_t)r * ORC_D);
+    }
+    free(part);
+}
+
 /* ---------------------------------------------------------------- gate ---------------------------------------- */
 
 void orc_gate(const float* att, const float* qf, int ntok, float* out) {

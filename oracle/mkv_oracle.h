@@ -68,6 +68,13 @@ void orc_attn_fa_mx(const uint16_t* kc, const uint16_t* vc, const float* q, int 
 void orc_attn_fa_f32(const float* kc, const float* vc, const float* q, int T, int n, int start, float scale,
                      const int* sel, int nsel, float* out);
 
+/* Small-block prefill (attn_fd4 + attn_fd_combine, ops.wgsl:694-778, 523-538; dispatched for blocks of fewer than 64
+ * tokens, engine.rs:1237-1241, with the uniforms of engine.rs:919-921: extra = 0, flag = PREFILL_BLOCK = 64): f32 Q
+ * against the cache (f16 values widened exactly), token t of the block sees [0, n + t), per block of bl positions an
+ * exact online max over tiles of 64, blocks merged with the log-sum-exp formula. q, out: [T][16][256]. */
+void orc_attn_fd4(int fmt, const void* kc, const void* vc, const float* q, int T, int n, float scale, int bl,
+                  float* out);
+
 /* Output gate, attn_gate (ops.wgsl:171-177): out[t][h*256+d] = att[t][h*256+d] * sigmoid(qf[t][h*512+256+d]). */
 void orc_gate(const float* att, const float* qf, int ntok, float* out);
 

@@ -37,6 +37,7 @@ def lib():
         _lib.orc_attn_dmx.argtypes = [P, P, P, I, I, F, I, P]
         _lib.orc_attn_fa_mx.argtypes = [P, P, P, I, I, I, F, I, P, I, P]
         _lib.orc_attn_fa_f32.argtypes = [P, P, P, I, I, I, F, P, I, P]
+        _lib.orc_attn_fd4.argtypes = [I, P, P, P, I, I, F, I, P]
         _lib.orc_gate.argtypes = [P, P, I, P]
         _lib.orc_rmsnorm_rows.argtypes = [P, I, I, P, F, P]
         _lib.orc_qk_norm_rope.argtypes = [P, P, I, P, P, F, P, P, P]
@@ -135,6 +136,16 @@ def attn_fa_f32(kc, vc, q, n, start=0, scale=1.0 / 16, sel=None):
     sel = _c(sel, np.int32)
     out = np.empty((len(sel), H, D), np.float32)
     lib().orc_attn_fa_f32(_p(kc), _p(vc), _p(q), T, int(n), int(start), float(scale), _p(sel), len(sel), _p(out))
+    return out
+
+
+def attn_fd4(fmt, kc, vc, q, n, scale=1.0 / 16, bl=64):
+    """Small-block prefill (attn_fd4, ops.wgsl:694-778): token t of the block sees [0, n + t)."""
+    q = _c(q, np.float32).reshape(-1, H, D)
+    T = q.shape[0]
+    assert n + T - 1 <= kc.shape[0] and bl % 64 == 0
+    out = np.empty((T, H, D), np.float32)
+    lib().orc_attn_fd4(int(fmt), _p(kc), _p(vc), _p(q), T, int(n), float(scale), int(bl), _p(out))
     return out
 
 

@@ -45,6 +45,25 @@ def assert_attn_close(got, ref, atol=ATOL, rtol=RTOL, what=""):
     return max_abs, rel
 
 
+SMALL_PREFILL_MAX = 63  # f16 blocks up to this many tokens run f32-class, as the reference's attn_fd4
+
+
+def prefill_reference(fmt, kc, vc, q, n0, start=0, sel=None):
+    """(reference rows, atol, rtol) of a prefill of the block q: the oracle function of the reference kernel the block
+    takes (engine.rs:1215-1241) and the bar it is held to. f32 store: attn_fa (exact f32), 1e-5; f16 store, blocks of
+    64 tokens or more: attn_fa_mx, the task tolerance; f16 blocks under 64 tokens: attn_fd4 (f32 Q, exact max; with a
+    window start, attn_fd per token, the same f32 arithmetic), 1e-5."""
+    T = np.asarray(q).reshape(-1, H, D).shape[0]
+    if sel is None:
+        sel = np.arange(T, dtype=np.int32)
+    if fmt == 1:
+        return O.attn_fa_f32(kc, vc, q, n0, start=start, sel=sel), 1e-5, 1e-5
+    if T > SMALL_PREFILL_MAX:
+        return O.attn_fa_mx(kc, vc, q, n0, start=start, sel=sel), ATOL, RTOL
+    full = O.attn_fd4(0, kc, vc, q, n0) if start == 0 else O.attn_fd(0, kc, vc, q, n0, start=start)
+    return full[sel], 1e-5, 1e-5
+
+
 def exact_attention(kc, vc, q, n, start=0, scale=1.0 / 16):
     """Textbook softmax attention in float64 (brute force), reference layout caches; token t sees [start, n + t)."""
     K = O.f16_bits_to_f32(kc) if kc.dtype == np.uint16 else kc

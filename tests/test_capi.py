@@ -57,6 +57,25 @@ def test_errors_without_gpu():
     assert lib.mkv_snapshot_bytes(None, 10) == 0
 
 
+def test_store_bytes_known_answer():
+    """The reference's one known-answer size (memcheck.rs:110-111): 22 buffers (K and V of 10 attention layers + the
+    MTP layer) of 65,536 f32 positions = 2,952,790,016 bytes. The planes of a store of those 11 layers are exactly
+    that (the blocked layout has no padding at a multiple of 1024 positions); the store allocates the stated
+    overhead on top: 64 KiB of slack, the decode partials (2 x 32 rows x 256 splits x 1,040 B) and the prefill
+    partials (2 x 4,096 (token, split) pairs x 8 heads x 1,040 B)."""
+    assert 2 * 11 * mk.buffer_bytes(65536, mk.F32) == 2_952_790_016
+    assert mk.buffer_bytes(65536, mk.F16) * 2 == mk.buffer_bytes(65536, mk.F32)
+    overhead = 65536 + 2 * 32 * 256 * 1040 + 2 * 4096 * 8 * 1040
+    assert mk.store_bytes(11, 65536, mk.F32) == 2_952_790_016 + overhead
+    # f16 halves the planes only; fewer decode splits below 16,256 positions
+    assert mk.store_bytes(11, 65536, mk.F16) == 2_952_790_016 // 2 + overhead
+    assert mk.store_bytes(1, 4096, mk.F16) == 4096 * 512 * 2 * 2 + 65536 + 2 * 32 * 66 * 1040 + 2 * 4096 * 8 * 1040
+    # cfg4: 10 f16 layers at 262,144 positions, 5.37 GB of planes
+    assert mk.store_bytes(10, 262144, mk.F16) - overhead == 5_368_709_120
+    # what mkv_create refuses has no size
+    assert mk.store_bytes(1, 5000, mk.F16) == 0 and mk.store_bytes(1, 4096, 3) == 0 and mk.store_bytes(0, 4096, 0) == 0
+
+
 # ---- root files: key and container parsing (host code only) ----
 
 def test_fnv1a64_published_vectors():

@@ -3,8 +3,8 @@
 (mkv_append_decode: fused append + decode + merge) and a prefill are captured through the C ABI on torch's capture
 stream and replayed several times, with eager work of the same store in between; every replay must equal the eager
 call of the same step bit for bit (a captured step re-appends its rows at the same positions, so replays are
-idempotent). The calls make no allocation, host synchronization or memset once the store exists (the prefill
-workspace is grown by one eager call before capture).
+idempotent). The calls make no allocation, host synchronization or memset once the store exists: the graph is
+captured before any eager attention call of the store.
 """
 import numpy as np
 import pytest
@@ -26,37 +26,41 @@ def test_captured_verify_and_prefill_replay_bit_identical(torch_gpu, fmt):
     import mechta_amd as mk
     torch = torch_gpu
     print(f"graph capture fmt={fmt}", flush=True)
-    n0, ntok, T = 3000, 4, 64
+    n0, ntok, T, Ts = 3000, 4, 64, 24
     kn, v = kv_inputs(71, n0 + T)
     tab = O.rope_tables(0, n0 + T)
-    q4, q64 = _dev(torch, q_inputs(72, ntok)), _dev(torch, q_inputs(73, T))
+    q4, q64, q24 = _dev(torch, q_inputs(72, ntok)), _dev(torch, q_inputs(73, T)), _dev(torch, q_inputs(74, Ts))
     with mk.KvStore(1, 8192, fmt) as st:
         for p in range(0, n0 - 1, 512):
             m = min(512, n0 - 1 - p)
             st.append(0, p, _dev(torch, kn[p:p + m]), _dev(torch, v[p:p + m]), _dev(torch, tab[p:p + m]))
         step_in = [_dev(torch, a[n0 - 1:n0 - 1 + ntok]) for a in (kn, v, tab)]
-        out_e = st.append_decode(0, n0, *step_in, q4).clone()
-        pf_e = st.prefill(0, q64, n0 + ntok - T).clone()  # the last T positions as a prefill block (grows ws)
-        st.set_len(n0 - 1)
         torch.cuda.synchronize()
-
-        out_g = torch.empty_like(out_e)
-        pf_g = torch.empty_like(pf_e)
+        # captured first, on a store that has run no attention yet: nothing is allocated or grown by the calls
+        out_g = torch.empty((ntok, 16, 256), device="cuda")
+        pf_g = torch.empty((T, 16, 256), device="cuda")
+        ps_g = torch.empty((Ts, 16, 256), device="cuda")
         g = torch.cuda.CUDAGraph()
         base_stream = torch.cuda.current_stream()
         with torch.cuda.graph(g):
             st.set_stream(torch.cuda.current_stream())
             st.append_decode(0, n0, *step_in, q4, out=out_g)
-            st.prefill(0, q64, n0 + ntok - T, out=pf_g)
+            st.prefill(0, q64, n0 + ntok - T, out=pf_g)   # the last T positions as a prefill block
+            st.prefill(0, q24, n0 + ntok - Ts, out=ps_g)  # a small block (f32-class on the f16 store)
         st.set_stream(base_stream)
+        st.set_len(n0 - 1)
+        out_e = st.append_decode(0, n0, *step_in, q4).clone()
+        pf_e = st.prefill(0, q64, n0 + ntok - T).clone()
+        ps_e = st.prefill(0, q24, n0 + ntok - Ts).clone()
         torch.cuda.synchronize()
         for r in range(4):
-            out_g.fill_(float("nan"))
-            pf_g.fill_(float("nan"))
+            for t in (out_g, pf_g, ps_g):
+                t.fill_(float("nan"))
             g.replay()
             torch.cuda.synchronize()
             assert torch.equal(out_g, out_e), f"replay {r}: verify output differs from the eager call"
             assert torch.equal(pf_g, pf_e), f"replay {r}: prefill output differs from the eager call"
+            assert torch.equal(ps_g, ps_e), f"replay {r}: small prefill output differs from the eager call"
             # eager work of the same store between replays: a decode at another length
             other = st.decode(0, q4, n0 - 500)
             torch.cuda.synchronize()

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import assert_attn_close, kv_inputs, q_inputs
+from tests.helpers import assert_attn_close, kv_inputs, prefill_reference, q_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -96,9 +96,5 @@ def test_sweep_prefill(torch_gpu, i, fmt, n0, T, start):
         out = st.prefill(0, _dev(torch, q), n0, start=start).cpu().numpy()
     kc, vc = O.new_cache(ctx, fmt), O.new_cache(ctx, fmt)
     O.append(fmt, kc, vc, 0, kn, v, tab)
-    if fmt == F32:
-        ref = O.attn_fa_f32(kc, vc, q, n0, start=start, sel=sel)
-        assert_attn_close(out[sel], ref, atol=1e-5, rtol=1e-5, what="f32 prefill")
-    else:
-        ref = O.attn_fa_mx(kc, vc, q, n0, start=start, sel=sel)
-        assert_attn_close(out[sel], ref, what="f16 prefill vs attn_fa_mx")
+    ref, atol, rtol = prefill_reference(fmt, kc, vc, q, n0, start=start, sel=sel)
+    assert_attn_close(out[sel], ref, atol=atol, rtol=rtol, what=f"prefill fmt {fmt} T {T}")

@@ -16,6 +16,10 @@ Function -> what pins it:
   orc_attn_fa_mx     float64 brute force; chunk size invariance (2048 vs 64); a selected subset of tokens equals the
                      same rows of the full call.
   orc_attn_fa_f32    float64 brute force within 1e-5.
+  orc_attn_fd4       float64 brute force within 1e-5 on both formats (f32 Q: the f16-Q prefill attn_fa_mx misses that
+                     bound on the same inputs); position-block size (64, 128, 512) does not change the result; one key
+                     -> v; identical keys -> mean of V; a key with a large score in a later tile (the running max
+                     moves and the earlier tiles are shrunk).
   orc_gate           sigmoid closed form at 0 (x/2), large positive (x), large negative (0).
 """
 import math
@@ -250,6 +254,46 @@ def test_attn_fa_f32_vs_f64():
     ex = exact_attention(kc, vc, q, 1000)
     ma, rel = err_stats(got, ex)
     assert ma < 1e-5 and rel < 1e-5
+
+
+@pytest.mark.parametrize("fmt", [F16, F32])
+@pytest.mark.parametrize("n,T", [(1, 8), (1000, 32), (2047, 37), (129, 63)])
+def test_attn_fd4_vs_f64(fmt, n, T):
+    kc, vc = _cache(fmt, n + T - 1, 80 + T + n)
+    q = np.random.default_rng(81 + T).standard_normal((T, 16, 256), dtype=np.float32)
+    got = O.attn_fd4(fmt, kc, vc, q, n)
+    ex = exact_attention(kc, vc, q, n)
+    ma, rel = err_stats(got, ex)
+    assert ma < 1e-5 and rel < 1e-5, (ma, rel)
+    for bl in (128, 512):
+        assert np.allclose(O.attn_fd4(fmt, kc, vc, q, n, bl=bl), got, atol=1e-6)
+    if fmt == F16 and n > 1:
+        # Q is not rounded to f16: the f16-Q prefill of the same block is measurably further from float64
+        ma16, _ = err_stats(O.attn_fa_mx(kc, vc, q, n), ex)
+        assert ma16 > 4 * ma
+
+
+def test_attn_fd4_special_cases():
+    kc, vc = _cache(F16, 200, 82)
+    q = np.random.default_rng(83).standard_normal((8, 16, 256), dtype=np.float32)
+    out = O.attn_fd4(F16, kc, vc, q, 1)  # token 0 sees one key
+    v0 = O.f16_bits_to_f32(vc[0])
+    for h in range(16):
+        assert np.allclose(out[0, h], v0[h // 8], atol=1e-6)
+    kc2 = kc.copy()
+    kc2[:150] = kc2[0]  # identical keys: uniform weights, the mean of V
+    out = O.attn_fd4(F16, kc2, vc, q[:1], 150)
+    mean = O.f16_bits_to_f32(vc[:150]).astype(np.float64).mean(axis=0)
+    for h in range(16):
+        assert np.allclose(out[0, h], mean[h // 8], atol=1e-5)
+    # a key in the third 64-position tile with score 40 above the rest: the running max moves past two tiles
+    kc3 = kc.copy()
+    c = 40 * 16 / np.dot(q[0, 3], q[0, 3])
+    kc3[140, 0] = (q[0, 3] * c).astype(np.float16).view(np.uint16)
+    out = O.attn_fd4(F16, kc3, vc, q, 150)
+    ma, rel = err_stats(out, exact_attention(kc3, vc, q, 150))
+    assert ma < 1e-5 and rel < 1e-5
+    assert np.allclose(out[0, 3], O.f16_bits_to_f32(vc[140, 0]), atol=1e-5)
 
 
 def test_gate_closed_form():
