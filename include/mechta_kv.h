@@ -122,6 +122,16 @@ int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* k_norme
                       const float* rope_tab, const float* q, int start, float scale, float* out,
                       const float* gate_src);
 
+/* mkv_append_decode with no allocation of any kind: for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. Same arguments, results
+ * bit-identical to mkv_append_decode; the split-K partials go to a scratch array of the library (16,506,880 bytes per
+ * GPU, held until the process ends) instead of the handle's workspace. Limit: at most 248 splits (every decode plan of
+ * 1..4 tokens fits; MKV_E_SIZE otherwise, nothing enqueued). The scratch is shared by every handle on one GPU: calls
+ * that overlap on one GPU (on different streams, or from different handles without ordering) race. */
+int mkv_append_decode_noalloc(mkv_t* h, int layer, int n, int ntok, const float* k_normed, const float* v,
+                              const float* rope_tab, const float* q, int start, float scale, float* out,
+                              const float* gate_src);
+
 /* Causal prefill attention of T (1..512) tokens of one layer: token t sees positions [start, n + t).
  *   q: [T][16][256] f32 (device); out: [T][16][256] f32 (device); gate_src as mkv_decode ([T][16][512]).
  * Requires n + T - 1 <= len(layer). Replaces q_f16 + attn_fa_mx + attn_fd_combine (fa_mx.wgsl:19-115, 313-319;

@@ -24,7 +24,8 @@ SYMBOLS = ["mkv_create", "mkv_destroy", "mkv_set_stream", "mkv_sync", "mkv_last_
            "mkv_append", "mkv_set_len", "mkv_decode", "mkv_append_decode", "mkv_prefill", "mkv_snapshot_bytes",
            "mkv_snapshot", "mkv_restore", "mkv_read_rows", "mkv_write_rows", "mkv_trace", "mkv_trace_read",
            "mkv_rope_table", "mkv_root_key", "mkv_root_save", "mkv_root_wait", "mkv_root_info", "mkv_root_load",
-           "mkv_rope_table_dev", "mkv_qk_norm_rope", "mkv_buffer_bytes", "mkv_store_bytes"]
+           "mkv_rope_table_dev", "mkv_qk_norm_rope", "mkv_buffer_bytes", "mkv_store_bytes",
+           "mkv_append_decode_noalloc"]
 SPAN_KV_WRITE, SPAN_CORE, SPAN_MERGE = 0, 1, 2
 
 
@@ -58,6 +59,7 @@ def lib():
             "mkv_set_len": ([P, I], I),
             "mkv_decode": ([P, I, P, I, I, I, F, P, P], I),
             "mkv_append_decode": ([P, I, I, I, P, P, P, P, I, F, P, P], I),
+            "mkv_append_decode_noalloc": ([P, I, I, I, P, P, P, P, I, F, P, P], I),
             "mkv_prefill": ([P, I, P, I, I, I, F, P, P], I),
             "mkv_snapshot_bytes": ([P, I], S),
             "mkv_snapshot": ([P, I, P, S], I),

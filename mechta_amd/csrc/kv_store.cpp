@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -37,6 +38,37 @@ namespace {
 
 using mkv::fail;
 using mkv::hip_fail;
+
+// Scratch of mkv_append_decode_noalloc: the split-K partials of one decode (2 kv heads x 32 rows x up to 248 splits x
+// 260 floats = 16,506,880 bytes), a file-scope device array instead of the handle's workspace, so that the call
+// allocates nothing. Each GPU holds its own copy until the process ends. Host code never uses the array's name as a
+// device address: its per-device address comes from hipGetSymbolAddress, resolved once per device by mkv_create
+// with that device current. Every call on one GPU shares it; calls that overlap on one GPU (other streams, other
+// handles) race. No part needs clearing: a decode reads only partials its own core launch wrote.
+constexpr int SCRATCH_CHUNKS = 248;
+constexpr size_t SCRATCH_FLOATS = (size_t)KVH * ROWS * SCRATCH_CHUNKS * PART;
+static __device__ __align__(256) float scratch[SCRATCH_FLOATS];
+constexpr int MAX_DEVICES = 64;
+float* g_scratch[MAX_DEVICES] = {};
+std::mutex g_scratch_mu;
+
+// Resolves (once) the scratch's address on `dev`, the current device.
+hipError_t resolve_scratch(int dev) {
+    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch[dev]) return hipSuccess;
+    float* p = nullptr;
+    hipError_t e = hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch[dev] = p;
+    return hipSuccess;
+}
+
+float* scratch_of(int dev) {
+    if (dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return g_scratch[dev];
+}
 
 int check_layer(const mkv_store* h, int layer) {
     if (layer < 0 || layer >= h->g.layers) return fail(MKV_E_LAYER, "layer %d outside [0, %d)", layer, h->g.layers);
@@ -73,26 +105,26 @@ hipError_t traced(mkv_store* h, int kind, F&& fn) {
     return e;
 }
 
-hipError_t decode_all(mkv_store* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
-                      const float* gate, const FusedAppend& fa = FusedAppend{}) {
+hipError_t decode_all(mkv_store* h, const DecodeWs& ws, int layer, const float* q, int ntok, int n, int start,
+                      float scale, float* out, const float* gate, const FusedAppend& fa = FusedAppend{}) {
     if (h->g.fmt == MKV_F32) {
         const Attn32Plan p = attn32_plan(ntok, n, start);
-        if (p.nch > h->dws.max_chunks) return hipErrorInvalidValue;
+        if (p.nch > ws.max_chunks) return hipErrorInvalidValue;
         hipError_t e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
-            return launch_attn_f32(h->g, h->base, layer, q, ntok, n, start, scale, p, ROWS, h->dws.part, fa, L);
+            return launch_attn_f32(h->g, h->base, layer, q, ntok, n, start, scale, p, ROWS, ws.part, fa, L);
         });
         if (e != hipSuccess) return e;
         return traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {
-            return launch_merge(h->dws.part, ROWS, ntok, n, start, p.span, p.nch, gate, out, L);
+            return launch_merge(ws.part, ROWS, ntok, n, start, p.span, p.nch, gate, out, L);
         });
     }
     DecodePlan p = decode_plan(n, ntok, start);
     hipError_t e = traced(h, MKV_SPAN_CORE, [&](const Launch& L) {
-        return launch_decode_core(h->g, h->base, layer, q, ntok, n, start, scale, p, h->dws, fa, L);
+        return launch_decode_core(h->g, h->base, layer, q, ntok, n, start, scale, p, ws, fa, L);
     });
     if (e != hipSuccess) return e;
     return traced(h, MKV_SPAN_MERGE,
-                  [&](const Launch& L) { return launch_decode_merge(ntok, n, start, p, h->dws, gate, out, L); });
+                  [&](const Launch& L) { return launch_decode_merge(ntok, n, start, p, ws, gate, out, L); });
 }
 
 // Floats of the prefill partials workspace, allocated with the store: the largest any prefill plan uses (the f16
@@ -164,8 +196,13 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
     if (ctx % 1024 != 0 || ctx < MKV_CTX_MIN || ctx > MKV_CTX_MAX)
         return fail(MKV_E_CTX, "context %d: must be a multiple of 1024 between %d and %d", ctx, MKV_CTX_MIN,
                     MKV_CTX_MAX);
+    int dev = 0;
+    hipError_t de = hipGetDevice(&dev);
+    if (de == hipSuccess) de = resolve_scratch(dev);
+    if (de != hipSuccess) return hip_fail(de, "mkv_create: scratch address of the current device");
     mkv_store* h = new (std::nothrow) mkv_store;
     if (!h) return fail(MKV_E_NOMEM, "mkv_create: host allocation");
+    h->device = dev;
     h->g.layers = layers;
     h->g.ctx = ctx;
     h->g.fmt = fmt;
@@ -298,40 +335,62 @@ static int check_attn(const mkv_t* h, const char* who, int layer, const float* q
 int mkv_decode(mkv_t* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
                const float* gate) {
     if (int rc = check_attn(h, "mkv_decode", layer, q, ntok, 4, n, start, out)) return rc;
-    hipError_t e = decode_all(h, layer, q, ntok, n, start, scale, out, gate);
+    hipError_t e = decode_all(h, h->dws, layer, q, ntok, n, start, scale, out, gate);
     return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_decode");
 }
 
-int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* kn, const float* v, const float* tab,
-                      const float* q, int start, float scale, float* out, const float* gate) {
-    if (ntok < 1 || ntok > 4) return fail(MKV_E_ARG, "mkv_append_decode: %d tokens outside [1, 4]", ntok);
-    if (!h || !kn || !v || !tab) return fail(MKV_E_ARG, "mkv_append_decode: NULL argument");
+static int append_decode(const char* who, mkv_t* h, const DecodeWs* ws, int layer, int n, int ntok, const float* kn,
+                         const float* v, const float* tab, const float* q, int start, float scale, float* out,
+                         const float* gate) {
+    if (ntok < 1 || ntok > 4) return fail(MKV_E_ARG, "%s: %d tokens outside [1, 4]", who, ntok);
+    if (!h || !kn || !v || !tab) return fail(MKV_E_ARG, "%s: NULL argument", who);
     if (int rc = check_layer(h, layer)) return rc;
     const int pos = n - 1;
     if (pos < 0 || pos + ntok > h->g.ctx)
-        return fail(MKV_E_POS, "mkv_append_decode: positions [%d, %d) outside the context %d", pos, pos + ntok,
-                    h->g.ctx);
+        return fail(MKV_E_POS, "%s: positions [%d, %d) outside the context %d", who, pos, pos + ntok, h->g.ctx);
     if (pos > h->len[layer])
-        return fail(MKV_E_POS, "mkv_append_decode: position %d leaves a hole after the written length %d", pos,
-                    h->len[layer]);
+        return fail(MKV_E_POS, "%s: position %d leaves a hole after the written length %d", who, pos, h->len[layer]);
     const int old_len = h->len[layer];
     h->len[layer] = pos + ntok;
-    if (int rc = check_attn(h, "mkv_append_decode", layer, q, ntok, 4, n, start, out)) {
+    if (int rc = check_attn(h, who, layer, q, ntok, 4, n, start, out)) {
         h->len[layer] = old_len;
         return rc;
     }
+    if (!ws) ws = &h->dws;
     FusedAppend fa;
     fa.kn = kn;
     fa.v = v;
     fa.tab = tab;
     fa.pos = pos;
     fa.ntok = ntok;
-    hipError_t e = decode_all(h, layer, q, ntok, n, start, scale, out, gate, fa);
+    hipError_t e = decode_all(h, *ws, layer, q, ntok, n, start, scale, out, gate, fa);
     if (e != hipSuccess) {
         h->len[layer] = old_len;
-        return hip_fail(e, "mkv_append_decode");
+        return hip_fail(e, who);
     }
     return MKV_OK;
+}
+
+int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* kn, const float* v, const float* tab,
+                      const float* q, int start, float scale, float* out, const float* gate) {
+    return append_decode("mkv_append_decode", h, nullptr, layer, n, ntok, kn, v, tab, q, start, scale, out, gate);
+}
+
+int mkv_append_decode_noalloc(mkv_t* h, int layer, int n, int ntok, const float* kn, const float* v,
+                              const float* tab, const float* q, int start, float scale, float* out,
+                              const float* gate) {
+    if (!h) return fail(MKV_E_ARG, "mkv_append_decode_noalloc: NULL handle");
+    float* sp = scratch_of(h->device);
+    if (!sp) return fail(MKV_E_HIP, "mkv_append_decode_noalloc: no scratch address for device %d", h->device);
+    // the split plan of this call, checked against the scratch's capacity before anything is enqueued
+    const int nch = h->g.fmt == MKV_F32 ? attn32_plan(ntok < 1 ? 1 : ntok, n, start).nch
+                                        : decode_plan(n, ntok < 1 ? 1 : ntok, start).nch;
+    if (nch > SCRATCH_CHUNKS)
+        return fail(MKV_E_SIZE, "mkv_append_decode_noalloc: %d splits exceed the scratch's %d (%zu bytes)", nch,
+                    SCRATCH_CHUNKS, SCRATCH_FLOATS * sizeof(float));
+    const DecodeWs ws{sp, SCRATCH_CHUNKS};
+    return append_decode("mkv_append_decode_noalloc", h, &ws, layer, n, ntok, kn, v, tab, q, start, scale, out,
+                         gate);
 }
 
 int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, float scale, float* out,

@@ -14,6 +14,7 @@ struct mkv_store {
     mkv::Geom g;
     void* base = nullptr;           // layers x {K, V} x 2 planes
     hipStream_t stream = nullptr;
+    int device = 0;                 // the device current at mkv_create
     std::vector<int> len;           // written positions per layer
     mkv::DecodeWs dws{nullptr, 0};
     float* pws = nullptr;           // prefill partials
