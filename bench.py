@@ -504,6 +504,11 @@ def probe_sweep(torch, nbytes=134348800, nbuf=10, reps=60):
                ("empty launch, sc1 tail, 8 sub-counters", 248, 512, -9, 1, 1, 0, 0),
                ("empty launch, sc1 tail, flags", 248, 512, -10, 1, 1, 0, 0),
                ("half the bytes (67 MB)", 248, 512, 2, 1, 1, 0, nbytes // 2 // unit * unit),
+               ("67 MB, 496 x 256 threads", 496, 256, 2, 1, 1, 0, nbytes // 2 // unit * unit),
+               ("67 MB, 248 x 256 threads", 248, 256, 2, 1, 1, 0, nbytes // 2 // unit * unit),
+               ("67 MB, 248 x 512, depth 1", 248, 512, 1, 1, 1, 0, nbytes // 2 // unit * unit),
+               ("67 MB, contiguous range per work-group", 248, 512, 2, 1, 0, 0, nbytes // 2 // unit * unit),
+               ("67 MB, 496 x 256, contiguous", 496, 256, 2, 1, 0, 0, nbytes // 2 // unit * unit),
                ("4x the bytes (537 MB, cfg4 per layer)", 248, 512, 2, 1, 1, 0, None)]
     rows = []
     for what, wgs, thr, depth, nt, rr, tail, nb in shapes:

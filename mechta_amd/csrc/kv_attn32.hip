@@ -40,9 +40,8 @@ struct Tile {
     f32x4 v[8];  // V: keys 16k + 8e + 4s .. +3 of dim 64w + 32c + l % 32 (index 4k + 2c + e)
 };
 
-// NBUF tiles in registers, NBUF - 1 of them loading while one computes (2: deeper prefetch measured slower from HBM,
-// 3 tiles 2 us and 4 tiles 5 us more per 16K-position decode)
-template <int NBUF>
+// Two tiles in registers, one loading while the other computes (deeper prefetch measured slower from HBM: 3 tiles 2 us
+// and 4 tiles 5 us more per 16K-position decode)
 __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
                                                 size_t plane_elems, const float* __restrict__ q, int T, int n,
                                                 int start, float scale2, int span, int nch, int c0, int nrb, int rpk,
@@ -77,6 +76,36 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
         tstep = nch;
     }
 
+    // tile j of this split starts at key lo + 32j, at the same byte offset j * 32 KB in both planes; loads of tile
+    // ntile (the prefetch after the last) lie past the resources and return zeros without a memory access
+    const unsigned rbytes = ntile > 0 ? (unsigned)((ntile - 1) * tstep + 1) * TILE_BYTES : 0u;
+    const rsrc_t kr = plane_rsrc(kplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
+    const rsrc_t vr = plane_rsrc(vplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
+    const unsigned kofs = ((16 * w + 2 * s) * TILE + r32) * 16;  // + (4k + e) * 512 B: dims 64w + 16k + 8s + 4e
+    const unsigned vofs = (s * HD + 64 * w + r32) * 16;            // + (4k + 2e) * 4 KB + c * 32 dims * 16 B
+    auto load = [&](Tile& X, int j) {
+        const unsigned base = (unsigned)(j * tstep) * TILE_BYTES;
+#pragma unroll
+        for (int i = 0; i < 8; i++) X.k[i] = bload4f(kr, base + kofs + ((i >> 1) * 4 + (i & 1)) * (TILE * 16));
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            X.v[i] = bload4f(vr, base + vofs + ((i >> 2) * 4 + 2 * (i & 1)) * (HD * 16) + ((i >> 1) & 1) * (32 * 16));
+    };
+
+    // Q's loads, then the first two tiles': loads complete in order, so the Q split below waits for Q only, and the
+    // tiles fly while Q is split into LDS and the fused append's rows are computed
+    f32x4 xq[4][2];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = tid + 256 * k, row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
+        const float* qr = q + ((size_t)min(t, T - 1) * QH + kvh * GQA + (row & 7)) * HD + d8;
+        xq[k][0] = *(const f32x4*)qr;
+        xq[k][1] = *(const f32x4*)(qr + 4);
+    }
+    Tile X[2];
+    load(X[0], 0);
+    load(X[1], 1);
+
     // Fused append (decode only: mkv_append_decode on the f32 store). The new rows [apos, apos + antok) lie in the
     // last one or two tiles; the work-group holding a tile computes its new rows here (the same arithmetic as
     // append_kernel) into LDS, patches them into that tile's K and V registers, and stores them to the planes after
@@ -99,36 +128,17 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
 
     __shared__ __attribute__((aligned(16))) _Float16 qh[ROWS][QPAD], ql[ROWS][QPAD];  // Q split: hi, lo
     __shared__ f32x4 sx[2][4][4][64];  // partial S^T: [tile parity][wave][register quad][lane]
-    for (int i = tid; i < ROWS * HD / 8; i += 256) {
-        const int row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
-        f32x4 x0 = f32x4{}, x1 = f32x4{};
-        if (t < T) {
-            const float* qr = q + ((size_t)t * QH + kvh * GQA + (row & 7)) * HD + d8;
-            x0 = *(const f32x4*)qr;
-            x1 = *(const f32x4*)(qr + 4);
-        }
+    __shared__ __attribute__((aligned(16))) float cfw[4][ROWS];  // each wave's rescale factors
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = tid + 256 * k, row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
+        const f32x4 x0 = t < T ? xq[k][0] : f32x4{}, x1 = t < T ? xq[k][1] : f32x4{};
         half8 hi, lo;
         split8(x0, x1, hi, lo);
         *(half8*)&qh[row][d8] = hi;
         *(half8*)&ql[row][d8] = lo;
     }
     __syncthreads();
-
-    // tile j of this split starts at key lo + 32j, at the same byte offset j * 32 KB in both planes; loads of tile
-    // ntile (the prefetch after the last) lie past the resources and return zeros without a memory access
-    const unsigned rbytes = ntile > 0 ? (unsigned)((ntile - 1) * tstep + 1) * TILE_BYTES : 0u;
-    const rsrc_t kr = plane_rsrc(kplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
-    const rsrc_t vr = plane_rsrc(vplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
-    const unsigned kofs = ((16 * w + 2 * s) * TILE + r32) * 16;  // + (4k + e) * 512 B: dims 64w + 16k + 8s + 4e
-    const unsigned vofs = (s * HD + 64 * w + r32) * 16;            // + (4k + 2e) * 4 KB + c * 32 dims * 16 B
-    auto load = [&](Tile& X, int j) {
-        const unsigned base = (unsigned)(j * tstep) * TILE_BYTES;
-#pragma unroll
-        for (int i = 0; i < 8; i++) X.k[i] = bload4f(kr, base + kofs + ((i >> 1) * 4 + (i & 1)) * (TILE * 16));
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            X.v[i] = bload4f(vr, base + vofs + ((i >> 2) * 4 + 2 * (i & 1)) * (HD * 16) + ((i >> 1) & 1) * (32 * 16));
-    };
 
     const int vis = n + t0 + (r32 >> 3);  // lane's row sees keys < vis (and of this split, < hi)
     float m_run = NEG_INF, l_run = 0.f;
@@ -159,11 +169,11 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
             const half8 bl = *(const half8*)&ql[r32][64 * w + 16 * k + 8 * s];
             S = mfma3(kh, kl, bh, bl, S);
         }
+        float sv[16];
         f32x4(&sg)[4][4][64] = sx[j & 1];
 #pragma unroll
         for (int a = 0; a < 4; a++) sg[w][a][lane] = f32x4{S[4 * a], S[4 * a + 1], S[4 * a + 2], S[4 * a + 3]};
         lds_barrier();  // parity buffers: a group's round i + 2 writes pb again only after every wave passed round i + 1
-        float sv[16];
 #pragma unroll
         for (int a = 0; a < 4; a++) {
             const f32x4 p0 = sg[0][a][lane], p1 = sg[1][a][lane];
@@ -171,35 +181,47 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
 #pragma unroll
             for (int b = 0; b < 4; b++) sv[4 * a + b] = (p0[b] + p1[b]) + (p2[b] + p3[b]);
         }
-        // exact-max online softmax in log2 units; masked scores are -inf (selected, never computed from K)
+        // exact-max online softmax in log2 units on the raw scores (scale2 > 0: the max of the scaled scores is the
+        // scaled max, and the exponent is one FMA); masked scores are -inf. A tile that lies inside every row's window
+        // (the common case) takes no mask.
         float mt = NEG_INF;
+        if (!(k0 >= start && k0 + TILE <= n + t0 && k0 + TILE <= hi)) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int key = k0 + 8 * (i >> 2) + 4 * s + (i & 3);
-            sv[i] = (key >= start && key < vis && key < hi) ? sv[i] * scale2 : NEG_INF;
-            mt = fmaxf(mt, sv[i]);
+            for (int i = 0; i < 16; i++) {
+                const int key = k0 + 8 * (i >> 2) + 4 * s + (i & 3);
+                sv[i] = (key >= start && key < vis && key < hi) ? sv[i] : NEG_INF;
+            }
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+#pragma unroll
+        for (int i = 0; i < 16; i++) mt = fmaxf(mt, sv[i]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32)) * scale2;
         const float mn = fmaxf(m_run, mt);
         const float base = mn == NEG_INF ? 0.f : mn;
         const float cf = m_run == NEG_INF ? 0.f : fast_exp2(m_run - mn);
         float ls = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            sv[i] = fast_exp2(sv[i] - base);
+            sv[i] = fast_exp2(__builtin_fmaf(sv[i], scale2, -base));
             ls += sv[i];
         }
         ls += __shfl_xor(ls, 32);
         l_run = l_run * cf + ls;
         m_run = mn;
-        // rescale O: register i of this lane holds row 8(i/4) + 4s + i%4, whose factor lane (that row) holds
+        // rescale O: register i of this lane holds row 8(i/4) + 4s + i%4; the rows' factors pass through this wave's
+        // LDS row (four 16-byte reads at constant offsets)
         if (__builtin_amdgcn_ballot_w64(cf != 1.f)) {
+            if (s == 0) cfw[w][r32] = cf;
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float f = __shfl(cf, 8 * (i >> 2) + 4 * s + (i & 3));
-                O[0][i] *= f;
-                O[1][i] *= f;
+            for (int a = 0; a < 4; a++) {
+                const f32x4 f = *(const f32x4*)&cfw[w][8 * a + 4 * s];
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    O[0][4 * a + b] *= f[b];
+                    O[1][4 * a + b] *= f[b];
+                }
             }
+            __builtin_amdgcn_wave_barrier();
         }
         // keys past the block's last (unwritten or stale rows) have P = 0 and must not bring NaN in through V
         if (k0 + TILE > hi) {
@@ -223,17 +245,15 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
         }
     };
 
+    // two tiles in flight from the start: step(j) computes tile j while tile j + 1 loads; its buffer then takes the
+    // loads of tile j + 2
     const int rounds = ntile;
-    Tile X[NBUF];
-#pragma unroll
-    for (int b = 0; b < NBUF - 1; b++) load(X[b], b);
-    for (int i = 0; i < rounds; i += NBUF) {
-#pragma unroll
-        for (int b = 0; b < NBUF; b++) {
-            if (i + b >= rounds) break;
-            load(X[(b + NBUF - 1) % NBUF], i + b + NBUF - 1);
-            step(X[b], i + b);
-        }
+    for (int i = 0; i < rounds; i += 2) {
+        step(X[0], i);
+        load(X[0], i + 2);
+        if (i + 1 >= rounds) break;
+        step(X[1], i + 1);
+        load(X[1], i + 3);
     }
 
     // the fused append's rows into the planes, for the launches that follow
@@ -288,7 +308,7 @@ hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const flo
     const float* vp = (const float*)(b + g.plane(layer, 1, 0) * g.plane_bytes());
     if (T > 4) return hipErrorInvalidValue;  // decode only: prefill_f32 serves blocks
     dim3 grid(p.nrb * (p.nch - p.c0) * KVH);
-    return launch(attn_f32<2>, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
+    return launch(attn_f32, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
                   p.nch, p.c0, p.nrb, rpk, part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
 }
 
