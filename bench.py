@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--probe-sweep", action="store_true",
                     help="only the plain-read probe over launch shapes (work-groups, threads, loads in flight, load "
                          "policy, stage order, a tail write), as a markdown table")
+    ap.add_argument("--cfg5-only", action="store_true",
+                    help="only configs[4] (f32 store: snapshot, restore, verify, prefill), as one JSON line (profiling)")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="no GPU work: group a rocprofv3 --kernel-trace csv by kernel and grid (launches, mean, median, "
                          "min, max microseconds) as a markdown table")
@@ -580,6 +582,16 @@ def main():
         sys.exit(1)
     if args.probe_sweep:
         probe_sweep(torch)
+        return
+    if args.cfg5_only:
+        r = bench_cfg5(torch, mk)
+        if args.calib_copy:
+            src = torch.ones(64 << 20, device="cuda")
+            dst = torch.empty_like(src)
+            for _ in range(5):
+                torch.add(src, 0.0, out=dst)
+            torch.cuda.synchronize()
+        print(json.dumps({"cfg5": r}), flush=True)
         return
     dec = bench_decode(torch, mk, args.steps, args.warmup)
     ms_step = dec["ms"] / dec["steps"]
