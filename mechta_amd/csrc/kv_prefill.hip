@@ -28,10 +28,7 @@ namespace {
 constexpr int RB = MKV_PF_RB;                 // 32-row blocks (4 tokens x 8 heads) per wave
 constexpr int NW = MKV_PF_NW;                 // waves per work-group
 constexpr int PT = NW * 4 * RB;               // tokens per work-group
-#ifndef MKV_PF_SUB
-#define MKV_PF_SUB 1
-#endif
-constexpr int SUB = MKV_PF_SUB;               // 32-key subtiles per ring slot (per barrier)
+constexpr int SUB = 1;                        // 32-key subtiles per ring slot (per barrier)
 constexpr int TILE_BYTES = 32 * HD * 2;       // one 32-key K block (or its 4 V groups), f16
 constexpr int SLOT_BYTES = 2 * SUB * TILE_BYTES;  // K blocks, then V groups of a slot
 #ifndef MKV_PF_NSLOT
@@ -134,20 +131,11 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
         for (int i = tid; i < 32 * SUB * HD; i += NW * 64)
             if (k0 + (i >> 11) * 8 + (i & 7) >= kend) Vz[i] = 0;  // group i / 2048, position i % 8 in the group
     };
-    for (int j = 0; j < ntiles; j++) {
-        wait_tiles(min(ntiles - 1 - j, NSLOT - 2));
-        lds_barrier();  // tile j is in LDS for every wave; every wave is done with tile j - 1
-        if (j + NSLOT - 1 < ntiles) issue(j + NSLOT - 1);  // into the slot of tile j - 1
-        if (cs + 32 * SUB * (j + 1) > kend) {
-            zero_tail(j);
-            lds_barrier();
-        }
-#pragma unroll
-      for (int u = 0; u < SUB; u++) {
-        const int k0 = cs + 32 * (SUB * j + u);
-        if (k0 >= ce) break;
-        const unsigned char* Ks = ring + (j % NSLOT) * SLOT_BYTES + u * TILE_BYTES;
-        const unsigned char* Vs = ring + (j % NSLOT) * SLOT_BYTES + (SUB + u) * TILE_BYTES;
+    // S of tile j, the mask where it crosses a row's window, the online softmax (lazy reference max, O rescaled when a
+    // finite reference moved) and P into pa
+    auto s_soft = [&](int j, half8(&pa)[RB][2]) {
+        const int k0 = cs + 32 * j;
+        const unsigned char* Ks = ring + (j % NSLOT) * SLOT_BYTES;
         f32x16 Scur[RB];
 #pragma unroll
         for (int b = 0; b < RB; b++) Scur[b] = f32x16{};
@@ -170,7 +158,6 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, KP, 0);
-        half8 pa[RB][2];
 #pragma unroll
         for (int b = 0; b < RB; b++) {
             // the causal / start mask only where this tile crosses a row's window (raw scores; the scale, log2
@@ -221,6 +208,10 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             }
             lsum[b] = lsum[b] * cf + ls;
         }
+    };
+    // O += P . V of tile j
+    auto pv_tile = [&](int j, const half8(&pa)[RB][2]) {
+        const unsigned char* Vs = ring + (j % NSLOT) * SLOT_BYTES + TILE_BYTES;
         constexpr int VP = 3;  // V operands in flight ahead of the P.V MFMAs
         half8 vbuf[VP];
         auto vaddr = [&](int i) { return Vs + (2 * (i >> 3) + h) * 4096 + (32 * (i & 7) + r) * 16; };
@@ -240,7 +231,18 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, VP, 0);
-      }
+    };
+    for (int j = 0; j < ntiles; j++) {
+        wait_tiles(min(ntiles - 1 - j, NSLOT - 2));
+        lds_barrier();  // tile j is in LDS for every wave; every wave is done with tile j - 1
+        if (j + NSLOT - 1 < ntiles) issue(j + NSLOT - 1);  // into the slot of tile j - 1
+        if (cs + 32 * (j + 1) > kend) {
+            zero_tail(j);
+            lds_barrier();
+        }
+        half8 pa[RB][2];
+        s_soft(j, pa);
+        pv_tile(j, pa);
     }
 
     // partials of this wave's rows of present tokens: row index t*8 + head of the kv head, rows per kv head = 8T
