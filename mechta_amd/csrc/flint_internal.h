@@ -28,13 +28,15 @@ __host__ __device__ inline size_t v_off16(int r, int d) {
 }
 
 // Splits of one attention call: keys [klo, klo + span) (klo = the first token's window start rounded down to 32),
-// nch splits at chunk_lo boundaries, nrb token blocks (4 tokens; 32 for a prefill of more than 4).
+// nch splits at chunk_lo boundaries, nrb token blocks (4 tokens; 32 for a prefill of more than 4); fused: a decode
+// whose kernel merges its own few splits (no merge launch).
 struct Plan {
-    int klo, span, nch, nrb;
+    int klo, span, nch, nrb, fused;
 };
 constexpr int WS_ROWS = 16384;  // rows x splits per kv head that the split partials hold
+constexpr int WS_ARRIVALS = 64;  // floats after the partials: the fused decode's arrival counters (zero at creation)
 Plan plan(int pos0, int T, int win);
-size_t ws_floats();  // split partials of any plan: 4 kv heads x WS_ROWS x PART
+size_t ws_floats();  // split partials of any plan (4 kv heads x WS_ROWS x PART) and the arrival counters
 
 hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const float* q, int T, int pos0, int win,
                        const Plan& p, float* ws, const float* sinks, float* out, hipStream_t st);

@@ -33,6 +33,15 @@ namespace {
 #ifndef FL_DEC_NCH
 #define FL_DEC_NCH 64     // decode: splits per kv head at most
 #endif
+#ifndef FL_FUSE_NCH
+#define FL_FUSE_NCH 8     // decode with the merge fused (short spans): splits per kv head at most
+#endif
+#ifndef FL_FUSE_SPLIT
+#define FL_FUSE_SPLIT 64  // decode with the merge fused: positions per split at least
+#endif
+#ifndef FL_FUSE_SPAN
+#define FL_FUSE_SPAN 2048  // decode: spans up to this many positions merge in the kernel
+#endif
 
 constexpr int TILE = 32;
 constexpr int QPAD = HD + 8;  // LDS row of Q's halves: 16-byte reads of 32 rows conflict-free
@@ -664,7 +673,8 @@ template <int FMT, int NBUF>
 __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane, const void* __restrict__ vplane,
                                                 size_t plane_elems, int rows, const float* __restrict__ q, int T,
                                                 int pos0, int win, float scale2, int klo, int span, int nch,
-                                                float* __restrict__ part) {
+                                                float* __restrict__ part, unsigned* __restrict__ arrivals,
+                                                const float* __restrict__ sinks, float* __restrict__ out) {
     constexpr int BPE = FMT == 1 ? 4 : 2;
     const int c = blockIdx.x % nch, kvh = blockIdx.x / nch;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
@@ -828,39 +838,95 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
         ml[w][1][r16] = l_run;
     }
     __syncthreads();
-    if (w != 0) return;
-    const size_t rbase = (size_t)kvh * T * GQA;
+    // With the merge fused (arrivals != NULL, few splits), the partial is stored device-coherent (scope bit sc1,
+    // through the XCD's L2) and the kv head's last work-group to arrive merges them all; no work-group waits.
+    const bool fused = arrivals != nullptr;
+    __shared__ int last;
+    if (w == 0) {
+        const size_t rbase = (size_t)kvh * T * GQA;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int row = 4 * g + r;
-        float M = NEG_INF;
+        for (int r = 0; r < 4; r++) {
+            const int row = 4 * g + r;
+            float M = NEG_INF;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, ml[ww][0][row]);
-        float f[4];
+            for (int ww = 0; ww < 4; ww++) M = fmaxf(M, ml[ww][0][row]);
+            float f[4];
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) f[ww] = ml[ww][0][row] == NEG_INF ? 0.f : exp2f(ml[ww][0][row] - M);
-        if (row < T * GQA) {
-            float* p = part + ((rbase + row) * nch + c) * PART + PACC + r16;
+            for (int ww = 0; ww < 4; ww++) f[ww] = ml[ww][0][row] == NEG_INF ? 0.f : exp2f(ml[ww][0][row] - M);
+            if (row < T * GQA) {
+                float* p = part + ((rbase + row) * nch + c) * PART + PACC + r16;
 #pragma unroll
-            for (int cc = 0; cc < 8; cc++) {
-                float o = 0.f;
+                for (int cc = 0; cc < 8; cc++) {
+                    float o = 0.f;
 #pragma unroll
-                for (int ww = 0; ww < 4; ww++) o += f[ww] * ob[ww][cc][lane][r];
-                p[16 * cc] = o;
+                    for (int ww = 0; ww < 4; ww++) o += f[ww] * ob[ww][cc][lane][r];
+                    if (fused) __hip_atomic_store(p + 16 * cc, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else p[16 * cc] = o;
+                }
+            }
+        }
+        if (g == 0 && r16 < T * GQA) {
+            float M = NEG_INF, Lt = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) M = fmaxf(M, ml[ww][0][r16]);
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++)
+                Lt += ml[ww][0][r16] == NEG_INF ? 0.f : exp2f(ml[ww][0][r16] - M) * ml[ww][1][r16];
+            float* p = part + ((rbase + r16) * nch + c) * PART;
+            if (fused) {
+                __hip_atomic_store(p, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p + 1, Lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                p[0] = M;
+                p[1] = Lt;
+            }
+        }
+        if (fused) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial's stores are complete
+            int l = 0;
+            if (lane == 0) {
+                l = __hip_atomic_fetch_add(arrivals + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (unsigned)(nch - 1);
+                if (l) __hip_atomic_store(arrivals + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                last = l;
             }
         }
     }
-    if (g == 0 && r16 < T * GQA) {
-        float M = NEG_INF, Lt = 0.f;
+    if (!fused) return;
+    __syncthreads();
+    if (!last) return;
+    // the kv head's last work-group: the merge of fl_merge for its rows (row = token * 8 + head of the kv head, T * 8
+    // <= 16), thread = (row, 8 dims), every split's partial loaded in one round trip (device-coherent loads)
+    const int row = tid >> 4, d0 = (tid & 15) * 8;
+    if (row >= T * GQA) return;
+    const int head = kvh * GQA + (row & 7), t = row >> 3;
+    const rsrc_t pr = plane_rsrc(part + (size_t)kvh * T * GQA * nch * PART, (unsigned)(T * GQA * nch * PART * 4));
+    f32x4 hd[FL_FUSE_NCH], a0[FL_FUSE_NCH], a1[FL_FUSE_NCH];
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, ml[ww][0][r16]);
-#pragma unroll
-        for (int ww = 0; ww < 4; ww++)
-            Lt += ml[ww][0][r16] == NEG_INF ? 0.f : exp2f(ml[ww][0][r16] - M) * ml[ww][1][r16];
-        float* p = part + ((rbase + r16) * nch + c) * PART;
-        p[0] = M;
-        p[1] = Lt;
+    for (int cj = 0; cj < FL_FUSE_NCH; cj++) {
+        const unsigned off = cj < nch ? (unsigned)(((row * nch + cj) * PART) * 4) : 0x7FFFFFF0u;
+        hd[cj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 16));
+        a0[cj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off + (PACC + d0) * 4, 0, 16));
+        a1[cj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off + (PACC + d0 + 4) * 4, 0,
+                                                                                   16));
     }
+    const float sk = sinks ? sinks[head] * LOG2E : NEG_INF;
+    float M = sk;
+#pragma unroll
+    for (int cj = 0; cj < FL_FUSE_NCH; cj++)
+        if (cj < nch) M = fmaxf(M, hd[cj].x);
+    f32x4 s0 = f32x4{}, s1 = f32x4{};
+    float L = sinks && M != NEG_INF ? exp2f(sk - M) : 0.f;
+#pragma unroll
+    for (int cj = 0; cj < FL_FUSE_NCH; cj++) {
+        const float e = cj < nch && hd[cj].x != NEG_INF ? exp2f(hd[cj].x - M) : 0.f;
+        L += e * hd[cj].y;
+        s0 += e * a0[cj];
+        s1 += e * a1[cj];
+    }
+    float* o = out + ((size_t)t * QH + head) * HD + d0;
+    *(f32x4*)o = s0 / L;
+    *(f32x4*)(o + 4) = s1 / L;
 }
 
 // Merge for few splits (prefill blocks): 8 rows (token, head) per work-group of 256 threads, 4 dims per thread, the
@@ -907,7 +973,12 @@ Plan plan(int pos0, int T, int win) {
     const int klo = lo0 / 32 * 32, span = pos0 + T - klo;
     int nrb = (T + 3) / 4;
     int nch;
-    if (T <= 2) {  // fl_dec16
+    int fused = 0;
+    if (T <= 2 && span <= FL_FUSE_SPAN) {  // fl_dec16 merging its own partials: splits of at least FL_FUSE_SPLIT
+        nch = span / FL_FUSE_SPLIT;
+        nch = nch > FL_FUSE_NCH ? FL_FUSE_NCH : nch;
+        fused = 1;
+    } else if (T <= 2) {  // fl_dec16
         nch = span / FL_DEC_SPLIT;
         nch = nch > FL_DEC_NCH ? FL_DEC_NCH : nch;
     } else if (T <= 4) {  // one block of fl_attn: splits of at least 128 positions, 64 per kv head at most
@@ -921,10 +992,10 @@ Plan plan(int pos0, int T, int win) {
         nch = nch > room ? room : nch > 64 ? 64 : nch;
     }
     nch = nch < 1 ? 1 : nch;
-    return Plan{klo, span, nch, nrb};
+    return Plan{klo, span, nch, nrb, fused};
 }
 
-size_t ws_floats() { return (size_t)KVH * WS_ROWS * PART; }
+size_t ws_floats() { return (size_t)KVH * WS_ROWS * PART + WS_ARRIVALS; }
 
 hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const float* q, int T, int pos0, int win,
                        const Plan& p, float* ws, const float* sinks, float* out, hipStream_t st) {
@@ -934,21 +1005,26 @@ hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const 
     const dim3 grid(p.nrb * p.nch * KVH);
     const Launch L{st};
     hipError_t e;
-    if (T <= 2)  // decode (and 2-token steps): 16-row kernel
+    // arrival counters of the fused decode merge, zero between launches, after the partials
+    unsigned* arr = p.fused ? (unsigned*)(ws + (size_t)KVH * WS_ROWS * PART) : nullptr;
+    if (p.fused && p.nch > FL_FUSE_NCH) return hipErrorInvalidValue;
+    if (T <= 2) {  // decode (and 2-token steps): 16-row kernel
         e = fmt == 1 ? launch(fl_dec16<1, FL_DEC_BUF>, dim3(p.nch * KVH), dim3(256), L, kp, vp, pe, rows, q, T, pos0,
-                              win, scale2, p.klo, p.span, p.nch, ws)
+                              win, scale2, p.klo, p.span, p.nch, ws, arr, sinks, out)
                      : launch(fl_dec16<0, FL_DEC_BUF>, dim3(p.nch * KVH), dim3(256), L, kp, vp, pe, rows, q, T, pos0,
-                              win, scale2, p.klo, p.span, p.nch, ws);
-    else if (T <= 4)  // one block of 4 tokens
+                              win, scale2, p.klo, p.span, p.nch, ws, arr, sinks, out);
+        if (p.fused) return e;
+    } else if (T <= 4) {  // one block of 4 tokens
         e = fmt == 1 ? launch(fl_attn<1, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
                               p.span, p.nch, p.nrb, ws)
                      : launch(fl_attn<0, 2>, grid, dim3(256), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
                               p.span, p.nch, p.nrb, ws);
-    else  // prefill: 32-token blocks over an LDS ring
+    } else {  // prefill: 32-token blocks over an LDS ring
         e = fmt == 1 ? launch(fl_pf<1>, grid, dim3(PF_NW * 64), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
                               p.span, p.nch, ws)
                      : launch(fl_pf<0>, grid, dim3(PF_NW * 64), L, kp, vp, pe, rows, q, T, pos0, win, scale2, p.klo,
                               p.span, p.nch, ws);
+    }
     if (e != hipSuccess) return e;
     if (p.nch > 8 * MERGE_J) return hipErrorInvalidValue;
     if (p.nch <= MERGE_FEW)

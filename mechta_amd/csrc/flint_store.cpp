@@ -71,6 +71,7 @@ int mfl_create(mfl_t** out, int layers, int ctx, int fmt, const unsigned char* s
     hipError_t e = hipMalloc(&h->base, at);
     if (e == hipSuccess) e = hipMemsetAsync(h->base, 0, at, h->stream);
     if (e == hipSuccess) e = hipMalloc(&h->ws, fl::ws_floats() * sizeof(float));
+    if (e == hipSuccess) e = hipMemsetAsync(h->ws, 0, fl::ws_floats() * sizeof(float), h->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
     if (e != hipSuccess) {
         (void)hipGetLastError();
