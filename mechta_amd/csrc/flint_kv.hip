@@ -905,10 +905,10 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
 #pragma unroll
     for (int cj = 0; cj < FL_FUSE_NCH; cj++) {
         const unsigned off = cj < nch ? (unsigned)(((row * nch + cj) * PART) * 4) : 0x7FFFFFF0u;
-        hd[cj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 16));
-        a0[cj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off + (PACC + d0) * 4, 0, 16));
-        a1[cj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off + (PACC + d0 + 4) * 4, 0,
-                                                                                   16));
+        const unsigned oa = off + (PACC + d0) * 4;
+        hd[cj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, LOAD_SC1));
+        a0[cj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, oa, 0, LOAD_SC1));
+        a1[cj] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, oa + 16, 0, LOAD_SC1));
     }
     const float sk = sinks ? sinks[head] * LOG2E : NEG_INF;
     float M = sk;

@@ -103,6 +103,9 @@ __device__ inline rsrc_t plane_rsrc(const void* base, unsigned bytes) {
 // the streamed planes do not displace other lines (measured per launch from HBM: f16 decode 25.0 against 26.0 us,
 // f32 decode about 1 us less, Flint f32 decode 32 against 34 us).
 constexpr int LOAD_NT = 2;
+// Policy bit sc1 (16): a device-coherent load, for split partials another work-group of the same launch stored with
+// agent-scope atomic stores (the fused merges of the decodes).
+constexpr int LOAD_SC1 = 16;
 __device__ inline half8 bload16(rsrc_t r, unsigned off) {
     return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, LOAD_NT));
 }
