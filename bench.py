@@ -285,9 +285,7 @@ def bench_cfg1(torch, mk, steps):
     q, gate = seeded_normal(torch, gen, (1, 16, 256)), seeded_normal(torch, gen, (1, 16, 512))
     tab = rope_tabs(torch, mk, N0, N0 + 1)
     out = torch.empty((1, 16, 256), device="cuda")
-    for _ in range(10):
-        st.append_decode(0, N0 + 1, kn, v, tab, q, out=out, gate_src=gate)
-    torch.cuda.synchronize()
+    warm(torch, lambda: st.append_decode(0, N0 + 1, kn, v, tab, q, out=out, gate_src=gate), ms=30.0)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
