@@ -484,7 +484,8 @@ def probe_sweep(torch, nbytes=134348800, nbuf=10, reps=60):
     bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(nbuf)]
     torch.cuda.synchronize()
     ptrs = (ctypes.c_void_p * nbuf)(*[b.data_ptr() for b in bufs])
-    # (what, work-groups, threads, depth, non-temporal, round robin, tail bytes (+ store policy 0..3), bytes)
+    # (what, work-groups, threads, depth, non-temporal, round robin (2 + k: skew of k + 1 stages), tail bytes (+ store
+    # policy 0..3), bytes)
     shapes = [("empty launch", 248, 512, 2, 1, 1, 0, 0),
               ("default: 248 x 512, 2 stages in flight, nt, round robin", 248, 512, 2, 1, 1, 0, nbytes)]
     shapes += [(f"depth {d}", 248, 512, d, 1, 1, 0, nbytes) for d in (1, 3, 4)]
@@ -514,6 +515,9 @@ def probe_sweep(torch, nbytes=134348800, nbuf=10, reps=60):
                ("empty launch, sc1 fused-merge tail only", 248, 512, -6, 1, 1, 0, 0),
                ("empty launch, sc1 tail, 8 sub-counters", 248, 512, -9, 1, 1, 0, 0),
                ("empty launch, sc1 tail, flags", 248, 512, -10, 1, 1, 0, 0),
+               ("skew 2: half the work-groups 2 stages more, half 2 fewer", 248, 512, 2, 1, 3, 0, nbytes),
+               ("skew 2 + tail write 33 KB", 248, 512, 2, 1, 3, 33280, nbytes),
+               ("skew 3 + tail write 33 KB", 248, 512, 2, 1, 4, 33280, nbytes),
                ("half the bytes (67 MB)", 248, 512, 2, 1, 1, 0, nbytes // 2 // unit * unit),
                ("67 MB, 496 x 256 threads", 496, 256, 2, 1, 1, 0, nbytes // 2 // unit * unit),
                ("67 MB, 248 x 256 threads", 248, 256, 2, 1, 1, 0, nbytes // 2 // unit * unit),

@@ -22,16 +22,21 @@ __device__ inline __amdgpu_buffer_rsrc_t rsrc(const char* base, unsigned bytes) 
     return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
 }
 
-template <int DEPTH, int POL, bool RR>
-__global__ void __launch_bounds__(1024) probe_read(const char* __restrict__ p, unsigned nst, unsigned* __restrict__ out,
-                                                   unsigned tail_words, int tail_pol) {
+template <int DEPTH, int POL, bool RR, int MAXT>  // MAXT: the launch's threads at most (the register budget follows)
+__global__ void __launch_bounds__(MAXT) probe_read(const char* __restrict__ p, unsigned nst, unsigned* __restrict__ out,
+                                                   unsigned tail_words, int tail_pol, unsigned skew) {
     const unsigned nwg = gridDim.x, c = blockIdx.x, t = threadIdx.x, nt = blockDim.x;
     const unsigned stage = nt * LOADS * 16;
-    const unsigned per = (nst + nwg - 1) / nwg;
+    const unsigned per0 = (nst + nwg - 1) / nwg;
+    // skew (round robin, even nwg): the first per0 - skew rounds go to every work-group, the last 2 skew rounds' stages
+    // to the odd work-groups only, so half the grid ends skew stages early and the other half skew stages late
+    const unsigned base = skew ? (per0 - skew) * nwg : 0;
+    const unsigned per = !skew ? per0 : (c & 1) ? per0 + skew : per0 - skew;
     u32x4 acc = {0, 0, 0, 0};
     u32x4 b[DEPTH][LOADS];
     auto load = [&](unsigned j, u32x4* bb) {  // stage j of this work-group; past the end: out of range, no bytes
-        const unsigned u = RR ? j * nwg + c : c * per + j;
+        const unsigned u = !RR ? c * per + j : j < per0 - skew || !skew ? j * nwg + c
+                                                                         : base + (j - (per0 - skew)) * (nwg / 2) + c / 2;
         const bool ok = j < per && u < nst;
         const __amdgpu_buffer_rsrc_t r = rsrc(p + (size_t)(ok ? u : 0) * stage, ok ? stage : 0);
 #pragma unroll
@@ -249,13 +254,18 @@ __global__ void __launch_bounds__(512) probe_fused(const char* __restrict__ p, u
 }
 
 int g_tail_pol = 0;
+unsigned g_skew = 0;
 
 template <int DEPTH, int POL, bool RR>
 hipError_t launch_one(const char* p, unsigned nst, unsigned* out, unsigned tail_words, int wgs, int threads,
                       hipEvent_t a, hipEvent_t b) {
-    void* args[] = {(void*)&p, (void*)&nst, (void*)&out, (void*)&tail_words, (void*)&g_tail_pol};
-    return hipExtLaunchKernel((const void*)probe_read<DEPTH, POL, RR>, dim3(wgs), dim3(threads), args, 0, nullptr, a,
-                              b, 0);
+    void* args[] = {(void*)&p, (void*)&nst, (void*)&out, (void*)&tail_words, (void*)&g_tail_pol, (void*)&g_skew};
+    // the kernel built for the smallest thread bound that holds the launch: at 1024 threads a lane has 128 registers,
+    // which 3 or 4 stages in flight (96 or 128 of them for the loads alone) would spill
+    const void* k = threads <= 256   ? (const void*)probe_read<DEPTH, POL, RR, 256>
+                    : threads <= 512 ? (const void*)probe_read<DEPTH, POL, RR, 512>
+                                     : (const void*)probe_read<DEPTH, POL, RR, 1024>;
+    return hipExtLaunchKernel(k, dim3(wgs), dim3(threads), args, 0, nullptr, a, b, 0);
 }
 
 template <int POL, bool RR>
@@ -310,6 +320,9 @@ extern "C" int mkv_probe_run(const void* const* bufs, int nbuf, size_t bytes, in
         return (int)hipErrorInvalidValue;
     // the tail's store policy rides in the low bits of tail_bytes (a multiple of 16 plus 0..3)
     g_tail_pol = (int)(tail_bytes & 3);
+    // rr >= 2: round robin with a skew of rr - 1 stages between the two halves of the grid (even wgs)
+    g_skew = rr >= 2 ? (unsigned)(rr - 1) : 0u;
+    if (g_skew && (wgs % 2 || (size_t)g_skew * wgs >= bytes / stage)) return (int)hipErrorInvalidValue;
     tail_bytes &= ~(size_t)3;
     const unsigned nst = (unsigned)(bytes / stage), tail_words = (unsigned)(tail_bytes / 4);
     unsigned* out = nullptr;
