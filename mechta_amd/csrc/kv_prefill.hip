@@ -341,29 +341,52 @@ __global__ void __launch_bounds__(P32_NW * 64) prefill_f32(const float* __restri
         lds_barrier();  // tile j is in LDS for every wave; every wave is done with tile j - 1 and its S exchange
         if (j + 1 < ntiles) issue(j + 1);  // into the slot of tile j - 1
         const int k0 = cs + 32 * j;
-        const unsigned char* Ks = ring + (j & 1) * P32_SLOT;
-        const unsigned char* Vs = Ks + P32_TILE;
-        if (k0 + 32 > kend) {  // V rows past the written length may hold anything: zero them (0 * V stays finite)
-            float* Vz = (float*)Vs;
-            for (int i = tid; i < 32 * HD; i += P32_NW * 64)
-                if (k0 + (i / (4 * HD)) * 4 + (i & 3) >= kend) Vz[i] = 0.f;
-            lds_barrier();
+        unsigned char* Ks = ring + (j & 1) * P32_SLOT;
+        unsigned char* Vs = Ks + P32_TILE;
+        // The tile's f32 K and V split once, in place, into f16 hi + lo (the 4 row blocks' waves then read the split
+        // operands instead of each splitting the same tile): each thread takes 2 K and 2 V pairs of 16-byte chunks
+        // that hold 8 consecutive dims of one key (K chunks d/4 = 2g and 2g + 1) or 8 consecutive keys of one dim
+        // (V groups 2g and 2g + 1), and writes hi over the first chunk and lo over the second, where the operand
+        // reads below find them. V rows past the written length are zeroed on the way (0 * V stays finite).
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int pk = tid + P32_NW * 64 * u;  // K pair: chunk index 2 (pk / 32) of key pk % 32
+            unsigned char* a = Ks + ((2 * (pk >> 5)) * 32 + (pk & 31)) * 16;
+            half8 hi, lo;
+            split8(*(const f32x4*)a, *(const f32x4*)(a + 512), hi, lo);
+            const int pv = tid + P32_NW * 64 * u;  // V pair: groups 2 (pv / 256), +1 of dim pv % 256
+            unsigned char* b = Vs + ((2 * (pv >> 8)) * HD + (pv & 255)) * 16;
+            f32x4 v0 = *(const f32x4*)b, v1 = *(const f32x4*)(b + HD * 16);
+            if (k0 + 32 > kend) {
+                const int key = k0 + 8 * (pv >> 8);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    v0[e] = key + e < kend ? v0[e] : 0.f;
+                    v1[e] = key + 4 + e < kend ? v1[e] : 0.f;
+                }
+            }
+            half8 vh, vl;
+            split8(v0, v1, vh, vl);
+            *(half8*)a = hi;
+            *(half8*)(a + 512) = lo;
+            *(half8*)b = vh;
+            *(half8*)(b + HD * 16) = vl;
         }
+        lds_barrier();  // every pair split before any wave reads an operand
         f32x16 Sh = f32x16{}, Sl = f32x16{};
         constexpr int KP = 2;
-        f32x4 kb[KP][2];
+        half8 kb[KP][2];
 #pragma unroll
         for (int s = 0; s < KP; s++) {
-            kb[s][0] = *(const f32x4*)(Ks + kaddr + s * 2048);
-            kb[s][1] = *(const f32x4*)(Ks + kaddr + s * 2048 + 512);
+            kb[s][0] = *(const half8*)(Ks + kaddr + s * 2048);
+            kb[s][1] = *(const half8*)(Ks + kaddr + s * 2048 + 512);
         }
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-            half8 kh, kl;
-            split8(kb[s % KP][0], kb[s % KP][1], kh, kl);
+            const half8 kh = kb[s % KP][0], kl = kb[s % KP][1];
             if (s + KP < 8) {
-                kb[s % KP][0] = *(const f32x4*)(Ks + kaddr + (s + KP) * 2048);
-                kb[s % KP][1] = *(const f32x4*)(Ks + kaddr + (s + KP) * 2048 + 512);
+                kb[s % KP][0] = *(const half8*)(Ks + kaddr + (s + KP) * 2048);
+                kb[s % KP][1] = *(const half8*)(Ks + kaddr + (s + KP) * 2048 + 512);
             }
             Sh = mfma32(kh, qh[s], Sh);
             Sl = mfma32(kh, ql[s], Sl);
@@ -421,19 +444,18 @@ __global__ void __launch_bounds__(P32_NW * 64) prefill_f32(const float* __restri
         // key step k: keys 16k + 8h .. +7 = V groups 4k + 2h, +1; dim block nb: dims 128dh + 32nb + r
         auto vaddr = [&](int i) { return Vs + ((4 * (i >> 2) + 2 * h) * HD + 128 * dh + 32 * (i & 3) + r) * 16; };
         constexpr int VP = 2;
-        f32x4 vb[VP][2];
+        half8 vb[VP][2];
 #pragma unroll
         for (int i = 0; i < VP; i++) {
-            vb[i][0] = *(const f32x4*)vaddr(i);
-            vb[i][1] = *(const f32x4*)(vaddr(i) + HD * 16);
+            vb[i][0] = *(const half8*)vaddr(i);
+            vb[i][1] = *(const half8*)(vaddr(i) + HD * 16);
         }
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            half8 vh, vl;
-            split8(vb[i % VP][0], vb[i % VP][1], vh, vl);
+            const half8 vh = vb[i % VP][0], vl = vb[i % VP][1];
             if (i + VP < 8) {
-                vb[i % VP][0] = *(const f32x4*)vaddr(i + VP);
-                vb[i % VP][1] = *(const f32x4*)(vaddr(i + VP) + HD * 16);
+                vb[i % VP][0] = *(const half8*)vaddr(i + VP);
+                vb[i % VP][1] = *(const half8*)(vaddr(i + VP) + HD * 16);
             }
             O[i & 3] = mfma32(pl[i >> 2], vh, mfma32(ph[i >> 2], vl, mfma32(ph[i >> 2], vh, O[i & 3])));
         }
