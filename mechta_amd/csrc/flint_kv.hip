@@ -376,7 +376,39 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
         lds_barrier();  // slot j is in LDS for every wave; every wave is done with slot j - 1
         if (j + PF_NSLOT - 1 < ntiles) issue(j + PF_NSLOT - 1);  // into the slot of j - 1
         const int ks0 = lo + TILE * SUB * j;
-        if (ks0 < lo_first || ks0 + TILE * SUB > kend) {
+        if constexpr (FMT == 1) {
+            // the slot's f32 K and V split once, in place, into f16 hi + lo (the 8 waves then read split operands
+            // instead of each splitting the same tiles): a pair of 16-byte chunks holds 8 consecutive dims of one key
+            // (K chunks d/4 = 2g, 2g + 1) or 8 consecutive keys of one dim (V groups 2g, 2g + 1); hi goes over the
+            // first chunk and lo over the second, where the operand reads find them. V rows outside [lo_first, kend)
+            // are zeroed on the way (0 * V stays finite).
+            unsigned char* sl = ring + (j % PF_NSLOT) * SLOT;
+#pragma unroll
+            for (int u = 0; u < SUB; u++) {
+                static_assert(PF_NW * 64 == 512, "one K pair and one V pair per thread and tile");
+                const int pp = tid;  // 512 K pairs and 512 V pairs per tile
+                unsigned char* a = sl + u * TB + ((2 * (pp >> 5)) * 32 + (pp & 31)) * 16;
+                half8 kh, kl;
+                split8(*(const f32x4*)a, *(const f32x4*)(a + 512), kh, kl);
+                unsigned char* b = sl + (SUB + u) * TB + ((2 * (pp >> 7)) * HD + (pp & 127)) * 16;
+                f32x4 v0 = *(const f32x4*)b, v1 = *(const f32x4*)(b + HD * 16);
+                const int key = ks0 + TILE * u + 8 * (pp >> 7);
+                if (key < lo_first || key + 8 > kend) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        v0[e] = key + e >= lo_first && key + e < kend ? v0[e] : 0.f;
+                        v1[e] = key + 4 + e >= lo_first && key + 4 + e < kend ? v1[e] : 0.f;
+                    }
+                }
+                half8 vh, vl;
+                split8(v0, v1, vh, vl);
+                *(half8*)a = kh;
+                *(half8*)(a + 512) = kl;
+                *(half8*)b = vh;
+                *(half8*)(b + HD * 16) = vl;
+            }
+            lds_barrier();  // every pair split before any wave reads an operand
+        } else if (ks0 < lo_first || ks0 + TILE * SUB > kend) {
             zero_v(j);
             lds_barrier();
         }
@@ -389,20 +421,19 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
             // independent chains (Q hi; Q lo and K lo), added once: back-to-back MFMAs never wait on each other
             f32x16 Sh = f32x16{}, Sl = f32x16{};
             if constexpr (FMT == 1) {
-                constexpr int KP = 2;  // K operands (two f32x4 each) in flight ahead of the MFMAs
-                f32x4 kb[KP][2];
+                constexpr int KP = 2;  // K operands (hi and lo, split in the ring) in flight ahead of the MFMAs
+                half8 kb[KP][2];
 #pragma unroll
                 for (int s = 0; s < KP; s++) {
-                    kb[s][0] = *(const f32x4*)(Ks + kaddr + s * 2048);
-                    kb[s][1] = *(const f32x4*)(Ks + kaddr + s * 2048 + 512);
+                    kb[s][0] = *(const half8*)(Ks + kaddr + s * 2048);
+                    kb[s][1] = *(const half8*)(Ks + kaddr + s * 2048 + 512);
                 }
 #pragma unroll
                 for (int s = 0; s < 8; s++) {
-                    half8 kh, kl;
-                    split8(kb[s % KP][0], kb[s % KP][1], kh, kl);
+                    const half8 kh = kb[s % KP][0], kl = kb[s % KP][1];
                     if (s + KP < 8) {
-                        kb[s % KP][0] = *(const f32x4*)(Ks + kaddr + (s + KP) * 2048);
-                        kb[s % KP][1] = *(const f32x4*)(Ks + kaddr + (s + KP) * 2048 + 512);
+                        kb[s % KP][0] = *(const half8*)(Ks + kaddr + (s + KP) * 2048);
+                        kb[s % KP][1] = *(const half8*)(Ks + kaddr + (s + KP) * 2048 + 512);
                     }
                     Sh = mfma32(kh, qh[s], Sh);
                     Sl = mfma32(kh, ql[s], Sl);
@@ -479,19 +510,18 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
             if constexpr (FMT == 1) {
                 auto vaddr = [&](int i) { return Vs + (4 * (i >> 2) + 2 * h) * (HD * 16) + (32 * (i & 3) + r) * 16; };
                 constexpr int VP = 2;
-                f32x4 vbuf[VP][2];
+                half8 vbuf[VP][2];
 #pragma unroll
                 for (int i = 0; i < VP; i++) {
-                    vbuf[i][0] = *(const f32x4*)vaddr(i);
-                    vbuf[i][1] = *(const f32x4*)(vaddr(i) + HD * 16);
+                    vbuf[i][0] = *(const half8*)vaddr(i);
+                    vbuf[i][1] = *(const half8*)(vaddr(i) + HD * 16);
                 }
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    half8 vh, vl;
-                    split8(vbuf[i % VP][0], vbuf[i % VP][1], vh, vl);
+                    const half8 vh = vbuf[i % VP][0], vl = vbuf[i % VP][1];
                     if (i + VP < 8) {
-                        vbuf[i % VP][0] = *(const f32x4*)vaddr(i + VP);
-                        vbuf[i % VP][1] = *(const f32x4*)(vaddr(i + VP) + HD * 16);
+                        vbuf[i % VP][0] = *(const half8*)vaddr(i + VP);
+                        vbuf[i % VP][1] = *(const half8*)(vaddr(i + VP) + HD * 16);
                     }
                     O[i & 3] = mfma32(pl[i >> 2], vh, mfma32(ph[i >> 2], vl, mfma32(ph[i >> 2], vh, O[i & 3])));
                 }
