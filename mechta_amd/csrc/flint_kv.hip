@@ -248,7 +248,8 @@ __global__ void __launch_bounds__(256) fl_attn(const void* __restrict__ kplane, 
 // per 32 tokens, not once per 4. Per tile and wave:
 //   S^T[32 keys][32 rows] = K . Q^T   8 dim steps of v_mfma_f32_32x32x16_f16 (A = K rows in key_perm order from
 //                                     LDS; B = Q split hi + lo, in registers for the whole split): 2 passes on an
-//                                     f16 cache (K exact), 3 on an f32 cache (K split as it leaves LDS)
+//                                     f16 cache (K exact), 3 on an f32 cache (each ring slot's K and V split into
+//                                     f16 hi + lo once, in place, by the whole work-group)
 //   online softmax in registers with a lazy reference max (moves when first or when the tile maximum exceeds it by
 //   more than 8; the partial's m is that reference, which the merge treats like any other), f32 P
 //   O[32 rows][128] += P . V          2 key steps x 4 dim blocks (A = P split hi + lo from the S registers, B = V

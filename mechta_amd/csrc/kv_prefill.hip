@@ -276,7 +276,8 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
 // tokens. f32 operands are split into f16 hi + lo (hi.hi + hi.lo + lo.hi on v_mfma_f32_32x32x16_f16). Per tile and
 // wave:
 //   partial S^T[32 keys][32 rows] over the wave's 128 dims: 8 dim steps x 3 passes (A = K rows in key_perm order,
-//   split as they leave LDS; B = Q split once, in registers); the two halves are exchanged through LDS and added
+//   the tile's K and V split into hi + lo once, in place in the ring, by the whole work-group; B = Q split once, in
+//   registers); the two halves are exchanged through LDS and added
 //   (a + b in both waves, so both hold the same S)
 //   online softmax with a lazy reference max, redundantly in both waves of the pair
 //   O[32 rows][the wave's 128 dims] += P . V: 2 key steps x 4 dim blocks x 3 passes
