@@ -319,18 +319,24 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
 
     __shared__ __attribute__((aligned(16))) unsigned char ring[PF_NSLOT * SLOT];
     __shared__ __attribute__((aligned(16))) float cfs[PF_NW][32];  // rescale factors of a wave's rows
-    auto issue = [&](int j) {  // each wave copies 1/8 of every K and V tile of slot j
-        unsigned char* dst = ring + (j % PF_NSLOT) * SLOT + w * (TB / PF_NW);
+    // Each wave copies 1/8 of every K and V tile of slot j: K bytes [w TB/8, +TB/8). V: f16, the same; f32, dims
+    // [64 (w % 2), +64) of groups 2 (w / 2) and 2 (w / 2) + 1 (1 KB each), so that the V chunk pairs the wave splits
+    // below are its own copies (K's are in either layout).
+    const unsigned kreg = w * (TB / PF_NW);
+    const unsigned vreg0 = FMT == 1 ? (2 * (w >> 1)) * (HD * 16) + (w & 1) * (HD / 2 * 16) : kreg;
+    auto issue = [&](int j) {
+        unsigned char* dst = ring + (j % PF_NSLOT) * SLOT;
 #pragma unroll
         for (int u = 0; u < SUB; u++) {
             // a 32-position tile is one 32-row block of the ring (rows are a multiple of 32), K and V alike; tiles
             // past the split's end stay inside the plane and are never computed
-            const size_t off =
-                (size_t)((lo + TILE * (SUB * j + u)) % rows) * HD * Gm::BPE + w * (TB / PF_NW) + lane * 16;
+            const size_t off = (size_t)((lo + TILE * (SUB * j + u)) % rows) * HD * Gm::BPE + lane * 16;
 #pragma unroll
             for (int d = 0; d < Gm::DPT; d++) {
-                dma16(K + off + d * 1024, dst + u * TB + d * 1024);
-                dma16(V + off + d * 1024, dst + (SUB + u) * TB + d * 1024);
+                dma16(K + off + kreg + d * 1024, dst + u * TB + kreg + d * 1024);
+                // f32: d = 0, 1 are the two groups' 1 KB (DPT = 2); f16: the wave's 1 KB parts in order
+                const unsigned vo = FMT == 1 ? vreg0 + d * (HD * 16) : vreg0 + d * 1024;
+                dma16(V + off + vo, dst + (SUB + u) * TB + vo);
             }
         }
     };
@@ -373,27 +379,26 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
         }
     };
     for (int j = 0; j < ntiles; j++) {
-        pf_wait<PF_NSLOT - 2, Gm::LPT>(min(ntiles - 1 - j, PF_NSLOT - 2));
-        lds_barrier();  // slot j is in LDS for every wave; every wave is done with slot j - 1
-        if (j + PF_NSLOT - 1 < ntiles) issue(j + PF_NSLOT - 1);  // into the slot of j - 1
+        pf_wait<PF_NSLOT - 2, Gm::LPT>(min(ntiles - 1 - j, PF_NSLOT - 2));  // this wave's copies of slot j landed
         const int ks0 = lo + TILE * SUB * j;
         if constexpr (FMT == 1) {
-            // the slot's f32 K and V split once, in place, into f16 hi + lo (the 8 waves then read split operands
-            // instead of each splitting the same tiles): a pair of 16-byte chunks holds 8 consecutive dims of one key
-            // (K chunks d/4 = 2g, 2g + 1) or 8 consecutive keys of one dim (V groups 2g, 2g + 1); hi goes over the
-            // first chunk and lo over the second, where the operand reads find them. V rows outside [lo_first, kend)
-            // are zeroed on the way (0 * V stays finite).
+            // this wave's part of the slot's f32 K and V split once, in place, into f16 hi + lo (the 8 waves then read
+            // split operands instead of each splitting the same tiles): a pair of 16-byte chunks holds 8 consecutive
+            // dims of one key (K chunks d/4 = 2g, 2g + 1) or 8 consecutive keys of one dim (V groups 2g, 2g + 1); hi
+            // goes over the first chunk and lo over the second, where the operand reads find them. The pairs are the
+            // ones this wave copied, so no barrier comes between its copies and its split. V rows outside
+            // [lo_first, kend) are zeroed on the way (0 * V stays finite).
+            static_assert(TB / PF_NW == 2048 && HD / 2 * 16 == 1024, "2 KB of K and 2 x 1 KB of V per wave");
             unsigned char* sl = ring + (j % PF_NSLOT) * SLOT;
 #pragma unroll
             for (int u = 0; u < SUB; u++) {
-                static_assert(PF_NW * 64 == 512, "one K pair and one V pair per thread and tile");
-                const int pp = tid;  // 512 K pairs and 512 V pairs per tile
-                unsigned char* a = sl + u * TB + ((2 * (pp >> 5)) * 32 + (pp & 31)) * 16;
+                // K pair: chunk 4w + 2 (lane / 32) of key lane % 32; V pair: dim 64 (w % 2) + lane of groups 2 (w / 2), +1
+                unsigned char* a = sl + u * TB + ((4 * w + 2 * (lane >> 5)) * 32 + (lane & 31)) * 16;
                 half8 kh, kl;
                 split8(*(const f32x4*)a, *(const f32x4*)(a + 512), kh, kl);
-                unsigned char* b = sl + (SUB + u) * TB + ((2 * (pp >> 7)) * HD + (pp & 127)) * 16;
+                unsigned char* b = sl + (SUB + u) * TB + vreg0 + lane * 16;
                 f32x4 v0 = *(const f32x4*)b, v1 = *(const f32x4*)(b + HD * 16);
-                const int key = ks0 + TILE * u + 8 * (pp >> 7);
+                const int key = ks0 + TILE * u + 8 * (w >> 1);
                 if (key < lo_first || key + 8 > kend) {
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
@@ -408,8 +413,10 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
                 *(half8*)b = vh;
                 *(half8*)(b + HD * 16) = vl;
             }
-            lds_barrier();  // every pair split before any wave reads an operand
-        } else if (ks0 < lo_first || ks0 + TILE * SUB > kend) {
+        }
+        lds_barrier();  // slot j is in LDS (f32: split) for every wave; every wave is done with slot j - 1
+        if (j + PF_NSLOT - 1 < ntiles) issue(j + PF_NSLOT - 1);  // into the slot of j - 1
+        if (FMT == 0 && (ks0 < lo_first || ks0 + TILE * SUB > kend)) {
             zero_v(j);
             lds_barrier();
         }

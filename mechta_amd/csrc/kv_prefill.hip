@@ -307,13 +307,21 @@ __global__ void __launch_bounds__(P32_NW * 64) prefill_f32(const float* __restri
 
     __shared__ __attribute__((aligned(16))) unsigned char ring[2 * P32_SLOT];
     __shared__ __attribute__((aligned(16))) f32x4 xs[P32_NW][4][64];  // each wave's partial S^T
-    auto issue = [&](int j) {  // each wave copies 1/8 of tile j's K and V into slot j % 2
-        const size_t off = (size_t)(cs + 32 * j) * HD * 4 + w * (P32_TILE / P32_NW) + lane * 16;
-        unsigned char* dst = ring + (j & 1) * P32_SLOT + w * (P32_TILE / P32_NW);
+    // Each wave copies 1/8 of tile j's K and V into slot j % 2, chosen so that the 16-byte chunk pairs it later splits
+    // (below) are all its own: K bytes [4 KB w, +4 KB) (chunks d/4 = 8w .. 8w + 7 of every key), V dims
+    // [128 (w % 2), +128) of groups 2 (w / 2) and 2 (w / 2) + 1 (2 KB each).
+    const unsigned kreg = w * (P32_TILE / P32_NW);
+    const unsigned vreg0 = (2 * (w >> 1)) * (HD * 16) + (w & 1) * (HD / 2 * 16), vreg1 = vreg0 + HD * 16;
+    auto issue = [&](int j) {
+        const size_t off = (size_t)(cs + 32 * j) * HD * 4;
+        unsigned char* dst = ring + (j & 1) * P32_SLOT;
+        static_assert(P32_TILE / P32_NW == 4096 && HD / 2 * 16 == 2048, "4 KB of K and 2 x 2 KB of V per wave");
 #pragma unroll
-        for (int d = 0; d < P32_TILE / P32_NW / 1024; d++) {
-            dma16(K + off + d * 1024, dst + d * 1024);
-            dma16(V + off + d * 1024, dst + P32_TILE + d * 1024);
+        for (int d = 0; d < 4; d++) dma16(K + off + kreg + d * 1024 + lane * 16, dst + kreg + d * 1024);
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            dma16(V + off + vreg0 + d * 1024 + lane * 16, dst + P32_TILE + vreg0 + d * 1024);
+            dma16(V + off + vreg1 + d * 1024 + lane * 16, dst + P32_TILE + vreg1 + d * 1024);
         }
     };
     if (ntiles > 0) issue(0);
@@ -338,28 +346,26 @@ __global__ void __launch_bounds__(P32_NW * 64) prefill_f32(const float* __restri
     for (int nb = 0; nb < 4; nb++) O[nb] = f32x16{};
 
     for (int j = 0; j < ntiles; j++) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        lds_barrier();  // tile j is in LDS for every wave; every wave is done with tile j - 1 and its S exchange
-        if (j + 1 < ntiles) issue(j + 1);  // into the slot of tile j - 1
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile j have landed
         const int k0 = cs + 32 * j;
         unsigned char* Ks = ring + (j & 1) * P32_SLOT;
         unsigned char* Vs = Ks + P32_TILE;
-        // The tile's f32 K and V split once, in place, into f16 hi + lo (the 4 row blocks' waves then read the split
-        // operands instead of each splitting the same tile): each thread takes 2 K and 2 V pairs of 16-byte chunks
-        // that hold 8 consecutive dims of one key (K chunks d/4 = 2g and 2g + 1) or 8 consecutive keys of one dim
-        // (V groups 2g and 2g + 1), and writes hi over the first chunk and lo over the second, where the operand
-        // reads below find them. V rows past the written length are zeroed on the way (0 * V stays finite).
+        // This wave's part of tile j split once, in place, into f16 hi + lo (the 4 row blocks' waves then read split
+        // operands instead of each splitting the same tile): a pair of 16-byte chunks holds 8 consecutive dims of one
+        // key (K chunks d/4 = 2g, 2g + 1) or 8 consecutive keys of one dim (V groups 2g, 2g + 1); hi goes over the
+        // first chunk and lo over the second, where the operand reads below find them. The pairs are the ones this
+        // wave copied, so no barrier comes between its copies and its split. V rows past the written length are
+        // zeroed on the way (0 * V stays finite).
 #pragma unroll
         for (int u = 0; u < 2; u++) {
-            const int pk = tid + P32_NW * 64 * u;  // K pair: chunk index 2 (pk / 32) of key pk % 32
-            unsigned char* a = Ks + ((2 * (pk >> 5)) * 32 + (pk & 31)) * 16;
+            const int pk = lane + 64 * u;  // K pair pk: chunk 8w + 2 (pk / 32) of key pk % 32
+            unsigned char* a = Ks + ((8 * w + 2 * (pk >> 5)) * 32 + (pk & 31)) * 16;
             half8 hi, lo;
             split8(*(const f32x4*)a, *(const f32x4*)(a + 512), hi, lo);
-            const int pv = tid + P32_NW * 64 * u;  // V pair: groups 2 (pv / 256), +1 of dim pv % 256
-            unsigned char* b = Vs + ((2 * (pv >> 8)) * HD + (pv & 255)) * 16;
+            unsigned char* b = Vs + vreg0 + (lane + 64 * u) * 16;  // V pair: dim 128 (w % 2) + lane + 64u
             f32x4 v0 = *(const f32x4*)b, v1 = *(const f32x4*)(b + HD * 16);
             if (k0 + 32 > kend) {
-                const int key = k0 + 8 * (pv >> 8);
+                const int key = k0 + 8 * (w >> 1);
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     v0[e] = key + e < kend ? v0[e] : 0.f;
@@ -373,7 +379,8 @@ __global__ void __launch_bounds__(P32_NW * 64) prefill_f32(const float* __restri
             *(half8*)b = vh;
             *(half8*)(b + HD * 16) = vl;
         }
-        lds_barrier();  // every pair split before any wave reads an operand
+        lds_barrier();  // tile j is in LDS, split, for every wave; every wave is done with tile j - 1 and its exchange
+        if (j + 1 < ntiles) issue(j + 1);  // into the slot of tile j - 1
         f32x16 Sh = f32x16{}, Sl = f32x16{};
         constexpr int KP = 2;
         half8 kb[KP][2];
