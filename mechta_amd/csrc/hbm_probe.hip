@@ -3,8 +3,8 @@
 // a plain streaming read of the same bytes reaches on this GPU, and how that rate depends on the launch shape.
 //
 // Each of `wgs` work-groups (`threads` threads) reads stages of threads x 128 bytes (8 x 16-byte loads per thread),
-// dealt round robin (stage u to work-group u % wgs, as the decode deals its stages) or as one contiguous range per
-// work-group, with DEPTH stages in flight per work-group, 16-byte buffer loads (non-temporal or default policy), and
+// dealt round robin (stage u to work-group u % wgs, as the decode deals its stages; optionally skewed, half the
+// work-groups ending a few stages before the other half) or as one contiguous range per work-group, with DEPTH stages in flight per work-group, 16-byte buffer loads (non-temporal or default policy), and
 // folds the words with xor (written out only on an impossible value, so the loads stay live). Optionally every
 // work-group writes `tail` bytes at its end (as the decode writes its split-K partials), 16-byte stores with a chosen
 // cache policy. Durations come from the
@@ -305,7 +305,8 @@ hipError_t launch_any(int depth, int nt_policy, int rr, const char* p, unsigned 
 // the null stream. Launch shape: wgs work-groups of threads (64..1024) threads, depth (1..4) stages in flight (0:
 // probe_fused, the read followed by partials, a barrier per half of the grid and a merge read),
 // nt_policy != 0 for non-temporal loads, rr != 0 for stages dealt round robin (else one contiguous range per
-// work-group), tail_bytes written by each work-group at its end. *mean_us / *best_us: the launch durations from the
+// work-group; rr >= 2: round robin with the last 2 (rr - 1) rounds dealt to the odd work-groups only, a skew of rr - 1
+// stages between the grid's halves), tail_bytes written by each work-group at its end. *mean_us / *best_us: the launch durations from the
 // dispatch timestamps; *wall_us: the time per launch of reps launches enqueued back to back (events around them).
 // Returns 0, or a HIP error code.
 extern "C" int mkv_probe_run(const void* const* bufs, int nbuf, size_t bytes, int wgs, int threads, int depth,
