@@ -228,3 +228,45 @@ def test_captured_step_replay_bit_identical(torch_gpu, mf, fmt):
             st.attend(1, 700, q1, sinks)  # eager work of the same store between replays
             st.attend(0, pos0 - 1, q, sinks)
             torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("fmt", [F32, F16])
+@pytest.mark.parametrize("seed", [1, 2])
+def test_random_call_sequence(torch_gpu, mf, fmt, seed):
+    """A seeded sequence of ragged appends to a full and a sliding layer in step, with attention calls of 1 to 130
+    tokens ending at the written length on either layer in between (the sliding ring wraps several times): every
+    output against the oracle's attn_fd / attn_pf on its own caches fed the same appends, and the rings end
+    bit-identical."""
+    torch = torch_gpu
+    r = rng(500 + 10 * seed + fmt)
+    ctx = 8192
+    with mf.FlintStore(2, ctx, fmt, sliding=[False, True]) as st:
+        caches = [(O.fl_new_cache(st.rows(layer), fmt), O.fl_new_cache(st.rows(layer), fmt)) for layer in range(2)]
+        sinks = r.standard_normal(H, dtype=np.float32)
+        pos = 0
+        for step in range(40):
+            if pos < 600 or (r.random() < 0.4 and pos < ctx - 300):
+                m = int(r.integers(1, 300))
+                k = r.standard_normal((m, KVH, D), dtype=np.float32)
+                v = r.standard_normal((m, KVH, D), dtype=np.float32)
+                for layer in range(2):
+                    st.append(layer, pos, dev(torch, k), dev(torch, v))
+                    O.fl_kv_write(fmt, caches[layer][0], caches[layer][1], pos, k, v)
+                pos += m
+                continue
+            layer = int(r.integers(0, 2))
+            T = int(r.choice([1, 2, 3, 4, 8, 33, 64, 100, 130]))
+            pos0 = pos - T
+            print(f"flint sequence fmt={fmt} seed={seed} step {step}: layer {layer} T={T} pos0={pos0}", flush=True)
+            q = r.standard_normal((T, H, D), dtype=np.float32)
+            out = st.attend(layer, pos0, dev(torch, q), dev(torch, sinks)).cpu().numpy()
+            kc, vc = caches[layer]
+            win = 513 if layer == 1 else 0
+            ref = O.fl_attn_fd(fmt, kc, vc, q[0], pos0, win, sinks)[None] if T == 1 else \
+                O.fl_attn_pf(fmt, kc, vc, q, pos0, win, sinks)
+            assert_attn_close(out.reshape(ref.shape), ref, atol=TOL, rtol=TOL,
+                              what=f"step {step} layer {layer} T={T}")
+        for layer in range(2):
+            for which in range(2):
+                assert np.array_equal(rows_np(st, layer, which).reshape(-1),
+                                      caches[layer][which].reshape(-1)), f"layer {layer} plane {which} differs"
