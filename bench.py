@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--probe-sweep", action="store_true",
                     help="only the plain-read probe over launch shapes (work-groups, threads, loads in flight, load "
                          "policy, stage order, a tail write), as a markdown table")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="only the sustained dense f16 MFMA rate of the part (libmkv_probe.so), one JSON line")
     ap.add_argument("--cfg5-only", action="store_true",
                     help="only configs[4] (f32 store: snapshot, restore, verify, prefill), as one JSON line (profiling)")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
@@ -472,6 +474,23 @@ def bench_read_floor(torch, nbytes, nbuf=10, reps=60):
             "what": "one launch of a plain streaming read of the decode launch's K+V bytes (libmkv_probe.so)"}
 
 
+def bench_mfma_rate(wgs=512, iters=4000, reps=20):
+    """The dense f16 rate the matrix units sustain on this part with nothing else to do (libmkv_probe.so: every wave
+    runs 8 independent v_mfma_f32_32x32x16_f16 chains from registers, two waves per SIMD), after about 60 ms of the
+    same launches (the clock ramps under matrix work): the ceiling the prefill's roofline fraction, taken against the
+    published 2.5 PFLOP/s, is read beside."""
+    import ctypes
+    here = os.path.dirname(os.path.abspath(__file__))
+    probe = ctypes.CDLL(os.path.join(here, "mechta_amd", "lib", "libmkv_probe.so"))
+    tf, us = ctypes.c_float(), ctypes.c_float()
+    rc = probe.mkv_probe_mfma(wgs, iters, reps, ctypes.c_float(60.0), ctypes.byref(tf), ctypes.byref(us))
+    if rc != 0:
+        raise RuntimeError(f"mkv_probe_mfma failed: HIP error {rc}")
+    return {"tflops": round(tf.value, 1), "frac_of_peak": round(tf.value / F16_MFMA_PEAK_TFLOPS, 4),
+            "launch_us": round(us.value, 1),
+            "what": "dense f16 MFMA chains from registers only, 2 waves per SIMD, after a 60 ms warm-up"}
+
+
 def probe_sweep(torch, nbytes=134348800, nbuf=10, reps=60):
     """The plain-read probe (libmkv_probe.so) over launch shapes, for the bytes of one cfg2 decode launch, over nbuf
     buffers in turn (nothing from the last-level cache). Prints a markdown table: per shape the launch duration from
@@ -596,6 +615,9 @@ def main():
     if args.probe_sweep:
         probe_sweep(torch)
         return
+    if args.mfma_probe:
+        print(json.dumps({"mfma_sustained": bench_mfma_rate()}), flush=True)
+        return
     if args.cfg5_only:
         r = bench_cfg5(torch, mk)
         if args.calib_copy:
@@ -653,6 +675,7 @@ def main():
         res["cfg5"] = bench_cfg5(torch, mk)
         res["flint"] = bench_flint(torch, mk)
         res["hbm_read_floor"] = bench_read_floor(torch, int(core_bytes))
+        res["mfma_sustained"] = bench_mfma_rate()
     if args.calib_copy:
         # plain elementwise copy of a known size: its FETCH_SIZE / WRITE_SIZE counters give the scale from counter
         # units to bytes for the KV kernels' counters in the same run

@@ -392,3 +392,75 @@ extern "C" int mkv_probe_read(const void* const* bufs, int nbuf, size_t bytes, i
     float wall = 0.f;
     return mkv_probe_run(bufs, nbuf, bytes, wgs, 512, 2, 1, 1, 0, reps, mean_us, best_us, &wall);
 }
+
+// ---- the sustained rate of the f16 matrix units ----
+// Every wave runs `iters` rounds of 8 independent chains of v_mfma_f32_32x32x16_f16 (register operands, nothing
+// else), so the matrix units never wait on a dependence, memory or the vector units: the rate the part sustains at
+// the clock it holds under that load, the ceiling the prefill kernels' MFMA fraction is read against.
+namespace {
+typedef _Float16 mfma_h8 __attribute__((ext_vector_type(8)));
+typedef float mfma_f16v __attribute__((ext_vector_type(16)));
+
+__global__ void __launch_bounds__(256) probe_mfma(float* __restrict__ out, int iters) {
+    const int t = threadIdx.x;
+    mfma_h8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = (_Float16)((t * 7 + i) % 13 * 0.01f);
+        b[i] = (_Float16)((t * 3 + i) % 11 * 0.01f);
+    }
+    mfma_f16v c[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) c[k] = mfma_f16v{};
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) c[k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c[k], 0, 0, 0);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) s += c[k][0] + c[k][15];
+    if (s == 1234.5f) out[blockIdx.x] = s;  // never true for these operands: keeps the chains live
+}
+}  // namespace
+
+// Runs probe_mfma on wgs work-groups of 256 threads (8 per CU fill the matrix units: two waves per SIMD) for `iters`
+// rounds, first for about warm_ms of back-to-back launches (the clock ramps under sustained matrix work), then reps
+// timed launches. *tflops: dense f16 TFLOP/s of the timed launches (32,768 flop per MFMA); *us: their mean duration.
+extern "C" int mkv_probe_mfma(int wgs, int iters, int reps, float warm_ms, float* tflops, float* us) {
+    if (wgs < 1 || iters < 1 || reps < 1) return (int)hipErrorInvalidValue;
+    float* out = nullptr;
+    hipError_t e = hipMalloc(&out, (size_t)wgs * sizeof(float));
+    if (e != hipSuccess) return (int)e;
+    hipEvent_t a, b;
+    (void)hipEventCreate(&a);
+    (void)hipEventCreate(&b);
+    float ms = 0.f, warm = 0.f;
+    while (e == hipSuccess && warm < warm_ms) {  // warm-up: launches in batches of 8 until warm_ms have passed
+        e = hipEventRecord(a, nullptr);
+        for (int i = 0; i < 8 && e == hipSuccess; i++) {
+            hipLaunchKernelGGL(probe_mfma, dim3(wgs), dim3(256), 0, nullptr, out, iters);
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess) e = hipEventRecord(b, nullptr);
+        if (e == hipSuccess) e = hipEventSynchronize(b);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+        warm += ms;
+        if (ms <= 0.f) break;
+    }
+    if (e == hipSuccess) e = hipEventRecord(a, nullptr);
+    for (int i = 0; i < reps && e == hipSuccess; i++) {
+        hipLaunchKernelGGL(probe_mfma, dim3(wgs), dim3(256), 0, nullptr, out, iters);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipEventRecord(b, nullptr);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    (void)hipFree(out);
+    if (e != hipSuccess) return (int)e;
+    const double flop = (double)wgs * 4 * iters * 8 * 32768.0 * reps;  // 4 waves per work-group
+    *us = ms * 1e3f / reps;
+    *tflops = (float)(flop / (ms * 1e-3) / 1e12);
+    return 0;
+}
