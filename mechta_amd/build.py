@@ -1,5 +1,5 @@
 """Builds libmechta_kv.so (the HIP path and its C ABI) in-tree for gfx950 with hipcc, and libmkv_probe.so (bench.py's
-plain-read probe, no part of the ABI).
+plain-read and matrix-rate probes, no part of the ABI).
 
 Every HIP source is compiled with -Xclang -target-feature -Xclang -packed-fp32-ops (no packed-FP32 instructions) and
 linked into mechta_amd/lib/libmechta_kv.so. The library has no dependency on torch or on oracle/.

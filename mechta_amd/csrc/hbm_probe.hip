@@ -1,6 +1,7 @@
 // hbm_probe.hip -- measurement aid for bench.py, not part of the KV-cache ABI: the time one launch takes to read a
 // buffer of a given size from HBM with nothing else to do, so that the decode kernel's rate can be read against what
-// a plain streaming read of the same bytes reaches on this GPU, and how that rate depends on the launch shape.
+// a plain streaming read of the same bytes reaches on this GPU, and how that rate depends on the launch shape; and
+// (at the end of the file) the dense f16 rate the matrix units sustain, the same for the prefill kernels.
 //
 // Each of `wgs` work-groups (`threads` threads) reads stages of threads x 128 bytes (8 x 16-byte loads per thread),
 // dealt round robin (stage u to work-group u % wgs, as the decode deals its stages; optionally skewed, half the
