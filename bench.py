@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--probe-sweep", action="store_true",
                     help="only the plain-read probe over launch shapes (work-groups, threads, loads in flight, load "
                          "policy, stage order, a tail write), as a markdown table")
+    ap.add_argument("--flint-only", action="store_true",
+                    help="only the Flint KV path's figures (decode and prefill, full and sliding layers), one JSON line")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only the sustained dense f16 MFMA rate of the part (libmkv_probe.so), one JSON line")
     ap.add_argument("--cfg5-only", action="store_true",
@@ -614,6 +616,16 @@ def main():
         sys.exit(1)
     if args.probe_sweep:
         probe_sweep(torch)
+        return
+    if args.flint_only:
+        r = bench_flint(torch, mk)
+        if args.calib_copy:
+            src = torch.ones(64 << 20, device="cuda")
+            dst = torch.empty_like(src)
+            for _ in range(5):
+                torch.add(src, 0.0, out=dst)
+            torch.cuda.synchronize()
+        print(json.dumps({"flint": r}), flush=True)
         return
     if args.mfma_probe:
         print(json.dumps({"mfma_sustained": bench_mfma_rate()}), flush=True)
