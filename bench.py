@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--probe-sweep", action="store_true",
                     help="only the plain-read probe over launch shapes (work-groups, threads, loads in flight, load "
                          "policy, stage order, a tail write), as a markdown table")
+    ap.add_argument("--context-sweep", action="store_true",
+                    help="only the cfg2 step at contexts of 4K to 256K positions, a markdown table")
     ap.add_argument("--flint-only", action="store_true",
                     help="only the Flint KV path's figures (decode and prefill, full and sliding layers), one JSON line")
     ap.add_argument("--mfma-probe", action="store_true",
@@ -476,6 +478,59 @@ def bench_read_floor(torch, nbytes, nbuf=10, reps=60):
             "what": "one launch of a plain streaming read of the decode launch's K+V bytes (libmkv_probe.so)"}
 
 
+def context_sweep(torch, mk, steps=100):
+    """The cfg2 step (4-token verify with its fused append) at contexts from 4,096 to 262,144 positions, with enough
+    layers rotated that the K/V come from HBM (at least 512 MB in all): per context the step's µs, the decode kernel's
+    and the merge's µs from the library's dispatch timestamps, and the decode's rate over the K+V it must read.
+    Prints a markdown table."""
+    print("| positions | layers | step us | decode_f16 us | merge us | K+V MB | decode GB/s | of 8 TB/s |")
+    print("|---|---|---|---|---|---|---|---|")
+    NT = 4
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2040)
+    for n0 in (4096, 8192, 16384, 32768, 65536, 131072, 262140):
+        L = max(2, -(-(512 << 20) // (n0 * 2048)))
+        ctx = ((n0 + NT + 1023) // 1024) * 1024
+        st = mk.KvStore(L, ctx, mk.F16)
+        tabs = rope_tabs(torch, mk, 0, n0)
+        for layer in range(L):
+            fill_store(torch, mk, st, layer, n0, gen, tabs)
+        del tabs
+        kn, v = seeded_normal(torch, gen, (NT, 2, 256)), seeded_normal(torch, gen, (NT, 512))
+        q = seeded_normal(torch, gen, (NT, 16, 256))
+        tab = rope_tabs(torch, mk, n0, n0 + NT)
+        out = torch.empty((NT, 16, 256), device="cuda")
+        i = [0]
+
+        def step():
+            layer = i[0] % L
+            st.append_decode(layer, n0 + 1, kn, v, tab, q, out=out)
+            if layer == L - 1:
+                st.set_len(n0)  # every position's drafts rejected: the same work each round
+            i[0] += 1
+
+        warm(torch, step, ms=20.0)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / steps * 1000
+        st.trace(True)
+        for _ in range(steps):
+            step()
+        sp = st.trace_read()
+        st.trace(False)
+        st.close()
+        core = sp["core"][0] / sp["core"][1] * 1000
+        merge = sp["merge"][0] / max(1, sp["merge"][1]) * 1000
+        mb = (n0 + NT) * 2048 / 1e6
+        gbs = mb * 1e3 / core
+        print(f"| {n0 + NT} | {L} | {us:.2f} | {core:.2f} | {merge:.2f} | {mb:.1f} | {gbs:.0f} | "
+              f"{gbs / HBM_PEAK_GBS:.3f} |", flush=True)
+
+
 def bench_mfma_rate(wgs=512, iters=4000, reps=20):
     """The dense f16 rate the matrix units sustain on this part with nothing else to do (libmkv_probe.so: every wave
     runs 8 independent v_mfma_f32_32x32x16_f16 chains from registers, two waves per SIMD), after about 60 ms of the
@@ -616,6 +671,9 @@ def main():
         sys.exit(1)
     if args.probe_sweep:
         probe_sweep(torch)
+        return
+    if args.context_sweep:
+        context_sweep(torch, mk)
         return
     if args.flint_only:
         r = bench_flint(torch, mk)
