@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--probe-sweep", action="store_true",
                     help="only the plain-read probe over launch shapes (work-groups, threads, loads in flight, load "
                          "policy, stage order, a tail write), as a markdown table")
+    ap.add_argument("--prefill-sweep", action="store_true",
+                    help="only the prefill step at contexts of 0 to 100K positions and blocks of 64 to 512, a table")
     ap.add_argument("--context-sweep", action="store_true",
                     help="only the cfg2 step at contexts of 4K to 256K positions, a markdown table")
     ap.add_argument("--flint-only", action="store_true",
@@ -531,6 +533,54 @@ def context_sweep(torch, mk, steps=100):
               f"{gbs / HBM_PEAK_GBS:.3f} |", flush=True)
 
 
+def prefill_sweep(torch, mk):
+    """The cfg3 step (a 512-token block appended and prefilled) at contexts of 0 to 100,000 positions and blocks of 64
+    to 512 tokens at 28,000 positions, f16 and f32 stores: µs per step, the attention kernel's and the merge's µs from
+    the library's trace, and the kernel's TFLOP/s. Prints a markdown table."""
+    print("| store | positions before | tokens | step us | kernel us | merge us | kernel TFLOP/s | of 2.5 PFLOP/s |")
+    print("|---|---|---|---|---|---|---|---|")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2041)
+    for fmt, name in ((mk.F16, "f16"), (mk.F32, "f32")):
+        cases = [(0, 512), (2048, 512), (8192, 512), (28000, 512), (100000, 512), (28000, 64), (28000, 128)]
+        ctx = 101376
+        st = mk.KvStore(1, ctx, fmt)
+        for n0, T in cases:
+            tabs = rope_tabs(torch, mk, 0, n0 + T)
+            kn = seeded_normal(torch, gen, (n0 + T, 2, 256))
+            v = seeded_normal(torch, gen, (n0 + T, 512))
+            st.set_len(0)
+            for p0 in range(0, n0, 512):
+                m = min(512, n0 - p0)
+                st.append(0, p0, kn[p0:p0 + m], v[p0:p0 + m], tabs[p0:p0 + m])
+            q = seeded_normal(torch, gen, (T, 16, 256)) / 16.0
+
+            def step():
+                st.set_len(n0)
+                st.append(0, n0, kn[n0:n0 + T], v[n0:n0 + T], tabs[n0:n0 + T])
+                st.prefill(0, q, n0 + 1, scale=1.0)
+
+            warm(torch, step, ms=40.0)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                step()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / 10 * 1000
+            st.trace(True)
+            for _ in range(10):
+                step()
+            sp = st.trace_read()
+            st.trace(False)
+            core = sp["core"][0] / sp["core"][1] * 1000
+            merge = sp["merge"][0] / max(1, sp["merge"][1]) * 1000
+            tf = 4 * 256 * 16 * sum(n0 + t + 1 for t in range(T)) / (core * 1e-6) / 1e12
+            print(f"| {name} | {n0} | {T} | {us:.1f} | {core:.1f} | {merge:.1f} | {tf:.0f} | "
+                  f"{tf / F16_MFMA_PEAK_TFLOPS:.3f} |", flush=True)
+        st.close()
+
+
 def bench_mfma_rate(wgs=512, iters=4000, reps=20):
     """The dense f16 rate the matrix units sustain on this part with nothing else to do (libmkv_probe.so: every wave
     runs 8 independent v_mfma_f32_32x32x16_f16 chains from registers, two waves per SIMD), after about 60 ms of the
@@ -671,6 +721,9 @@ def main():
         sys.exit(1)
     if args.probe_sweep:
         probe_sweep(torch)
+        return
+    if args.prefill_sweep:
+        prefill_sweep(torch, mk)
         return
     if args.context_sweep:
         context_sweep(torch, mk)
