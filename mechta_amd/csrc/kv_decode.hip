@@ -470,6 +470,7 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
 
 // Merge for few chunks (prefill splits): a work-group of 256 threads merges 4 rows (token, head), 64 threads per
 // row, 4 dims per thread (16-byte loads); every group of MERGE_FEW chunks of the row is loaded in one round trip.
+template <bool GROUPS>  // false: at most MERGE_FEW chunks, one group
 __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part, int rpk, int ntok, int n, int start,
                                                  int span, int nch, const float* __restrict__ gate,
                                                  float* __restrict__ out) {
@@ -484,7 +485,7 @@ __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part,
     // (maximum, sum, accumulator); with one group this is the plain max-then-sum of the partials
     float M = NEG_INF, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int g0 = c0; g0 < c1; g0 += MERGE_FEW) {
+    for (int g0 = c0; GROUPS ? g0 < c1 : g0 == c0; g0 += MERGE_FEW) {
         float mj[MERGE_FEW], lj[MERGE_FEW];
         float4 aj[MERGE_FEW];
         float Mg = NEG_INF;
@@ -592,8 +593,11 @@ hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, 
     // few chunks, or many rows (prefill blocks) over up to two groups of chunks: a row per 64 threads (a 128-token
     // block at 28,000 positions, 32 splits, 87.8 against 94.2 us per step; with 64 splits, four groups, slower than
     // decode_combine: 68.4 against 63.0 us)
-    if (nch <= MERGE_FEW || (ntok >= 32 && nch <= 2 * MERGE_FEW))
-        return launch(merge_few, dim3((ntok * QH + 3) / 4), dim3(256), L, part, rpk, ntok, n, start, span, nch, gate,
+    if (nch <= MERGE_FEW)
+        return launch(merge_few<false>, dim3((ntok * QH + 3) / 4), dim3(256), L, part, rpk, ntok, n, start, span, nch,
+                      gate, out);
+    if (ntok >= 32 && nch <= 2 * MERGE_FEW)
+        return launch(merge_few<true>, dim3((ntok * QH + 3) / 4), dim3(256), L, part, rpk, ntok, n, start, span, nch, gate,
                       out);
     if (nch <= 16 * 9)
         return launch(decode_combine<9>, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, span, nch, gate,
