@@ -253,7 +253,7 @@ def test_append_decode_fused_entry(torch_gpu, mk, ctx, n0, fmt):
 
 @pytest.mark.parametrize("n0,T,start", [(2000, 64, 0), (100, 512, 0), (3000, 37, 0), (1, 16, 0), (2500, 96, 300),
                                         (3000, 63, 0), (1, 1, 0), (2001, 8, 0), (1000, 32, 0), (3500, 5, 0),
-                                        (3000, 29, 1234), (60, 2, 0)])
+                                        (3000, 29, 1234), (60, 2, 0), (2000, 64, 700)])
 def test_prefill_f16(torch_gpu, mk, n0, T, start):
     """Blocks of 64 tokens or more against attn_fa_mx (f16 Q), smaller blocks against attn_fd4 (f32 Q) at 1e-5."""
     torch = torch_gpu
@@ -271,7 +271,7 @@ def test_prefill_f16(torch_gpu, mk, n0, T, start):
 
 
 @pytest.mark.parametrize("n0,T,start", [(1500, 70, 0), (100, 512, 0), (2500, 96, 300), (1, 16, 0), (3000, 5, 0),
-                                        (40, 3, 0), (3500, 512, 2900)])
+                                        (40, 3, 0), (3500, 512, 2900), (1500, 70, 400)])
 def test_prefill_f32(torch_gpu, mk, n0, T, start):
     torch = torch_gpu
     print(f"prefill f32 n0={n0} T={T} start={start}", flush=True)
