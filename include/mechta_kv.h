@@ -122,6 +122,17 @@ int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* k_norme
                       const float* rope_tab, const float* q, int start, float scale, float* out,
                       const float* gate_src);
 
+/* mkv_decode / mkv_append_decode with the gated attention written as f16, the form the reference's 4-token verify
+ * (quad.rs:125) and its 2-token step with f16 activations (engine.rs:1103) hand to the f16 attn_output matvec:
+ * attn_gate16 (ops.wgsl:296-300), out16[t][h][d] = f16(attention * sigmoid(qf[h*512 + 256 + d])), rounded to nearest
+ * even (pack2x16float), as f16 bit patterns, [ntok][16][256] (device; the reference's [ntok][4096] halves).
+ * gate_src is required (MKV_E_ARG if NULL); every other argument and check as the f32 entry points. */
+int mkv_decode_g16(mkv_t* h, int layer, const float* q, int ntok, int n, int start, float scale, uint16_t* out16,
+                   const float* gate_src);
+int mkv_append_decode_g16(mkv_t* h, int layer, int n, int ntok, const float* k_normed, const float* v,
+                          const float* rope_tab, const float* q, int start, float scale, uint16_t* out16,
+                          const float* gate_src);
+
 /* mkv_append_decode with no allocation of any kind: for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. Same arguments, results
  * bit-identical to mkv_append_decode; the split-K partials go to a scratch array of the library (16,506,880 bytes per

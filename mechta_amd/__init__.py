@@ -25,7 +25,7 @@ SYMBOLS = ["mkv_create", "mkv_destroy", "mkv_set_stream", "mkv_sync", "mkv_last_
            "mkv_snapshot", "mkv_restore", "mkv_read_rows", "mkv_write_rows", "mkv_trace", "mkv_trace_read",
            "mkv_rope_table", "mkv_root_key", "mkv_root_save", "mkv_root_wait", "mkv_root_info", "mkv_root_load",
            "mkv_rope_table_dev", "mkv_qk_norm_rope", "mkv_buffer_bytes", "mkv_store_bytes",
-           "mkv_append_decode_noalloc"]
+           "mkv_append_decode_noalloc", "mkv_decode_g16", "mkv_append_decode_g16"]
 SPAN_KV_WRITE, SPAN_CORE, SPAN_MERGE = 0, 1, 2
 
 
@@ -60,6 +60,8 @@ def lib():
             "mkv_decode": ([P, I, P, I, I, I, F, P, P], I),
             "mkv_append_decode": ([P, I, I, I, P, P, P, P, I, F, P, P], I),
             "mkv_append_decode_noalloc": ([P, I, I, I, P, P, P, P, I, F, P, P], I),
+            "mkv_decode_g16": ([P, I, P, I, I, I, F, P, P], I),
+            "mkv_append_decode_g16": ([P, I, I, I, P, P, P, P, I, F, P, P], I),
             "mkv_prefill": ([P, I, P, I, I, I, F, P, P], I),
             "mkv_snapshot_bytes": ([P, I], S),
             "mkv_snapshot": ([P, I, P, S], I),
@@ -109,13 +111,14 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-def _dev(t, n, name):
-    """Checks a torch tensor argument: on a GPU, float32, contiguous, at least n elements."""
+def _dev(t, n, name, f16=False):
+    """Checks a torch tensor argument: on a GPU, float32 (float16 with f16), contiguous, at least n elements."""
     import torch
     if t.device.type != "cuda":
         raise ValueError(f"{name} must be a device tensor")
-    if t.dtype != torch.float32 or not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous float32")
+    want = torch.float16 if f16 else torch.float32
+    if t.dtype != want or not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous {str(want).split('.')[-1]}")
     if t.numel() < n:
         raise ValueError(f"{name} holds {t.numel()} values, {n} needed")
     return _ptr(t)
@@ -221,25 +224,32 @@ class KvStore:
     def set_len(self, n):
         _check(lib().mkv_set_len(self._h, n))
 
-    def decode(self, layer, q, n, start=0, scale=1.0 / 16, out=None, gate_src=None):
+    def decode(self, layer, q, n, start=0, scale=1.0 / 16, out=None, gate_src=None, f16_out=False):
+        """f16_out: the gated attention as float16 (mkv_decode_g16, the reference's attn_gate16); needs gate_src."""
         import torch
         ntok = q.numel() // (Q_HEADS * HEAD_DIM)
         if out is None:
-            out = torch.empty((ntok, Q_HEADS, HEAD_DIM), dtype=torch.float32, device=q.device)
+            out = torch.empty((ntok, Q_HEADS, HEAD_DIM), dtype=torch.float16 if f16_out else torch.float32,
+                              device=q.device)
         g = None if gate_src is None else _dev(gate_src, ntok * Q_HEADS * 512, "gate_src")
-        _check(lib().mkv_decode(self._h, layer, _dev(q, ntok * 4096, "q"), ntok, n, start, scale,
-                                _dev(out, ntok * 4096, "out"), g))
+        fn = lib().mkv_decode_g16 if f16_out else lib().mkv_decode
+        _check(fn(self._h, layer, _dev(q, ntok * 4096, "q"), ntok, n, start, scale,
+                  _dev(out, ntok * 4096, "out", f16_out), g))
         return out
 
-    def append_decode(self, layer, n, k_normed, v, rope_tab, q, start=0, scale=1.0 / 16, out=None, gate_src=None):
+    def append_decode(self, layer, n, k_normed, v, rope_tab, q, start=0, scale=1.0 / 16, out=None, gate_src=None,
+                      f16_out=False):
+        """f16_out as decode (mkv_append_decode_g16)."""
         import torch
         ntok = q.numel() // (Q_HEADS * HEAD_DIM)
         if out is None:
-            out = torch.empty((ntok, Q_HEADS, HEAD_DIM), dtype=torch.float32, device=q.device)
+            out = torch.empty((ntok, Q_HEADS, HEAD_DIM), dtype=torch.float16 if f16_out else torch.float32,
+                              device=q.device)
         g = None if gate_src is None else _dev(gate_src, ntok * Q_HEADS * 512, "gate_src")
-        _check(lib().mkv_append_decode(self._h, layer, n, ntok, _dev(k_normed, ntok * 512, "k_normed"),
-                                       _dev(v, ntok * 512, "v"), _dev(rope_tab, ntok * 64, "rope_tab"),
-                                       _dev(q, ntok * 4096, "q"), start, scale, _dev(out, ntok * 4096, "out"), g))
+        fn = lib().mkv_append_decode_g16 if f16_out else lib().mkv_append_decode
+        _check(fn(self._h, layer, n, ntok, _dev(k_normed, ntok * 512, "k_normed"), _dev(v, ntok * 512, "v"),
+                  _dev(rope_tab, ntok * 64, "rope_tab"), _dev(q, ntok * 4096, "q"), start, scale,
+                  _dev(out, ntok * 4096, "out", f16_out), g))
         return out
 
     def prefill(self, layer, q, n, start=0, scale=1.0 / 16, out=None, gate_src=None):

@@ -398,10 +398,11 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
 // Merge of the split-K partials: work-group (token, head, quarter of the dims); its 256 threads are 16 chunk lanes x
 // 16 dim lanes (4 dims each), so every chunk's 64 dims are one coalesced 256-byte read and all chunks are in flight at
 // once; the 16 chunk lanes are then summed in LDS.
-template <int MERGE_J>  // chunks per chunk lane: 9 for up to 144 splits, 16 for up to 256 (fewer loads when few)
+// H16: the output as f16 bits, rounded to nearest even (attn_gate16's pack2x16float, ops.wgsl:296-300), else f32.
+template <int MERGE_J, bool H16>  // chunks per chunk lane: 9 for up to 144 splits, 16 for up to 256
 __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ part, int rpk, int n, int start,
                                                       int span, int nch, const float* __restrict__ gate,
-                                                      float* __restrict__ out) {
+                                                      void* __restrict__ out) {
     const int t = blockIdx.x / QH, head = blockIdx.x % QH, dq = blockIdx.y, tid = threadIdx.x;
     const int kvh = head / GQA, row = t * GQA + head % GQA;
     const float* p = part + ((size_t)kvh * rpk + row) * nch * PART;
@@ -464,16 +465,18 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
             const float g = gate[((size_t)t * QH + head) * 512 + 256 + d];
             o = o * (1.f / (1.f + expf(-g)));
         }
-        out[((size_t)t * QH + head) * HD + d] = o;
+        const size_t oi = ((size_t)t * QH + head) * HD + d;
+        if constexpr (H16) ((unsigned short*)out)[oi] = f2h(o);
+        else ((float*)out)[oi] = o;
     }
 }
 
 // Merge for few chunks (prefill splits): a work-group of 256 threads merges 4 rows (token, head), 64 threads per
 // row, 4 dims per thread (16-byte loads); every group of MERGE_FEW chunks of the row is loaded in one round trip.
-template <bool GROUPS>  // false: at most MERGE_FEW chunks, one group
+template <bool GROUPS, bool H16>  // GROUPS false: at most MERGE_FEW chunks, one group; H16 as decode_combine
 __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part, int rpk, int ntok, int n, int start,
                                                  int span, int nch, const float* __restrict__ gate,
-                                                 float* __restrict__ out) {
+                                                 void* __restrict__ out) {
     const int rowid = blockIdx.x * 4 + (threadIdx.x >> 6);  // t * 16 + head
     if (rowid >= ntok * QH) return;
     const int t = rowid / QH, head = rowid % QH, d0 = (threadIdx.x & 63) * 4;
@@ -529,7 +532,13 @@ __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part,
         o.z *= 1.f / (1.f + expf(-g.z));
         o.w *= 1.f / (1.f + expf(-g.w));
     }
-    *(float4*)(out + ((size_t)t * QH + head) * HD + d0) = o;
+    const size_t oi = ((size_t)t * QH + head) * HD + d0;
+    if constexpr (H16) {
+        const unsigned lo = f2h(o.x) | (unsigned)f2h(o.y) << 16, hi = f2h(o.z) | (unsigned)f2h(o.w) << 16;
+        *(uint2*)((unsigned short*)out + oi) = make_uint2(lo, hi);
+    } else {
+        *(float4*)((float*)out + oi) = o;
+    }
 }
 
 }  // namespace
@@ -587,28 +596,32 @@ hipError_t launch_small_prefill(const Geom& g, const void* base, int layer, cons
                   32 * p.nzb, p.nzb);
 }
 
-hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,
-                        float* out, const Launch& L) {
+template <bool H16>
+hipError_t merge_as(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,
+                    void* out, const Launch& L) {
     if (nch > 16 * MERGE_JMAX) return hipErrorInvalidValue;
     // few chunks, or many rows (prefill blocks) over up to two groups of chunks: a row per 64 threads (a 128-token
     // block at 28,000 positions, 32 splits, 87.8 against 94.2 us per step; with 64 splits, four groups, slower than
     // decode_combine: 68.4 against 63.0 us)
+    const dim3 few((ntok * QH + 3) / 4), rows(ntok * QH, HD / 64);
     if (nch <= MERGE_FEW)
-        return launch(merge_few<false>, dim3((ntok * QH + 3) / 4), dim3(256), L, part, rpk, ntok, n, start, span, nch,
-                      gate, out);
+        return launch(merge_few<false, H16>, few, dim3(256), L, part, rpk, ntok, n, start, span, nch, gate, out);
     if (ntok >= 32 && nch <= 2 * MERGE_FEW)
-        return launch(merge_few<true>, dim3((ntok * QH + 3) / 4), dim3(256), L, part, rpk, ntok, n, start, span, nch, gate,
-                      out);
+        return launch(merge_few<true, H16>, few, dim3(256), L, part, rpk, ntok, n, start, span, nch, gate, out);
     if (nch <= 16 * 9)
-        return launch(decode_combine<9>, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, span, nch, gate,
-                      out);
-    return launch(decode_combine<MERGE_JMAX>, dim3(ntok * QH, HD / 64), dim3(256), L, part, rpk, n, start, span, nch,
-                  gate, out);
+        return launch(decode_combine<9, H16>, rows, dim3(256), L, part, rpk, n, start, span, nch, gate, out);
+    return launch(decode_combine<MERGE_JMAX, H16>, rows, dim3(256), L, part, rpk, n, start, span, nch, gate, out);
+}
+
+hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,
+                        void* out, bool h16, const Launch& L) {
+    return h16 ? merge_as<true>(part, rpk, ntok, n, start, span, nch, gate, out, L)
+               : merge_as<false>(part, rpk, ntok, n, start, span, nch, gate, out, L);
 }
 
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
-                               float* out, const Launch& L) {
-    return launch_merge(ws.part, ROWS, ntok, n, start, p.span, p.nch, gate, out, L);
+                               void* out, bool h16, const Launch& L) {
+    return launch_merge(ws.part, ROWS, ntok, n, start, p.span, p.nch, gate, out, h16, L);
 }
 
 }  // namespace mkv

@@ -105,8 +105,9 @@ hipError_t traced(mkv_store* h, int kind, F&& fn) {
     return e;
 }
 
+// out: f32, or f16 bits (h16, attn_gate16's output)
 hipError_t decode_all(mkv_store* h, const DecodeWs& ws, int layer, const float* q, int ntok, int n, int start,
-                      float scale, float* out, const float* gate, const FusedAppend& fa = FusedAppend{}) {
+                      float scale, void* out, bool h16, const float* gate, const FusedAppend& fa = FusedAppend{}) {
     if (h->g.fmt == MKV_F32) {
         const Attn32Plan p = attn32_plan(ntok, n, start);
         if (p.nch > ws.max_chunks) return hipErrorInvalidValue;
@@ -115,7 +116,7 @@ hipError_t decode_all(mkv_store* h, const DecodeWs& ws, int layer, const float* 
         });
         if (e != hipSuccess) return e;
         return traced(h, MKV_SPAN_MERGE, [&](const Launch& L) {
-            return launch_merge(ws.part, ROWS, ntok, n, start, p.span, p.nch, gate, out, L);
+            return launch_merge(ws.part, ROWS, ntok, n, start, p.span, p.nch, gate, out, h16, L);
         });
     }
     DecodePlan p = decode_plan(n, ntok, start);
@@ -124,7 +125,7 @@ hipError_t decode_all(mkv_store* h, const DecodeWs& ws, int layer, const float* 
     });
     if (e != hipSuccess) return e;
     return traced(h, MKV_SPAN_MERGE,
-                  [&](const Launch& L) { return launch_decode_merge(ntok, n, start, p, ws, gate, out, L); });
+                  [&](const Launch& L) { return launch_decode_merge(ntok, n, start, p, ws, gate, out, h16, L); });
 }
 
 // Floats of the prefill partials workspace, allocated with the store: the largest any prefill plan uses (the f16
@@ -321,7 +322,7 @@ int mkv_set_len(mkv_t* h, int len) {
 }
 
 static int check_attn(const mkv_t* h, const char* who, int layer, const float* q, int ntok, int maxtok, int n,
-                      int start, float* out) {
+                      int start, const void* out) {
     if (!h || !q || !out) return fail(MKV_E_ARG, "%s: NULL argument", who);
     if (int rc = check_layer(h, layer)) return rc;
     if (ntok < 1 || ntok > maxtok) return fail(MKV_E_ARG, "%s: %d tokens outside [1, %d]", who, ntok, maxtok);
@@ -332,18 +333,30 @@ static int check_attn(const mkv_t* h, const char* who, int layer, const float* q
     return MKV_OK;
 }
 
+static int decode_entry(const char* who, mkv_t* h, int layer, const float* q, int ntok, int n, int start, float scale,
+                        void* out, bool h16, const float* gate) {
+    if (int rc = check_attn(h, who, layer, q, ntok, 4, n, start, out)) return rc;
+    if (h16 && !gate) return fail(MKV_E_ARG, "%s: the f16 output is the gated attention: gate_src is required", who);
+    hipError_t e = decode_all(h, h->dws, layer, q, ntok, n, start, scale, out, h16, gate);
+    return e == hipSuccess ? MKV_OK : hip_fail(e, who);
+}
+
 int mkv_decode(mkv_t* h, int layer, const float* q, int ntok, int n, int start, float scale, float* out,
                const float* gate) {
-    if (int rc = check_attn(h, "mkv_decode", layer, q, ntok, 4, n, start, out)) return rc;
-    hipError_t e = decode_all(h, h->dws, layer, q, ntok, n, start, scale, out, gate);
-    return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_decode");
+    return decode_entry("mkv_decode", h, layer, q, ntok, n, start, scale, out, false, gate);
+}
+
+int mkv_decode_g16(mkv_t* h, int layer, const float* q, int ntok, int n, int start, float scale, uint16_t* out16,
+                   const float* gate) {
+    return decode_entry("mkv_decode_g16", h, layer, q, ntok, n, start, scale, out16, true, gate);
 }
 
 static int append_decode(const char* who, mkv_t* h, const DecodeWs* ws, int layer, int n, int ntok, const float* kn,
-                         const float* v, const float* tab, const float* q, int start, float scale, float* out,
-                         const float* gate) {
+                         const float* v, const float* tab, const float* q, int start, float scale, void* out,
+                         bool h16, const float* gate) {
     if (ntok < 1 || ntok > 4) return fail(MKV_E_ARG, "%s: %d tokens outside [1, 4]", who, ntok);
     if (!h || !kn || !v || !tab) return fail(MKV_E_ARG, "%s: NULL argument", who);
+    if (h16 && !gate) return fail(MKV_E_ARG, "%s: the f16 output is the gated attention: gate_src is required", who);
     if (int rc = check_layer(h, layer)) return rc;
     const int pos = n - 1;
     if (pos < 0 || pos + ntok > h->g.ctx)
@@ -363,7 +376,7 @@ static int append_decode(const char* who, mkv_t* h, const DecodeWs* ws, int laye
     fa.tab = tab;
     fa.pos = pos;
     fa.ntok = ntok;
-    hipError_t e = decode_all(h, *ws, layer, q, ntok, n, start, scale, out, gate, fa);
+    hipError_t e = decode_all(h, *ws, layer, q, ntok, n, start, scale, out, h16, gate, fa);
     if (e != hipSuccess) {
         h->len[layer] = old_len;
         return hip_fail(e, who);
@@ -373,7 +386,14 @@ static int append_decode(const char* who, mkv_t* h, const DecodeWs* ws, int laye
 
 int mkv_append_decode(mkv_t* h, int layer, int n, int ntok, const float* kn, const float* v, const float* tab,
                       const float* q, int start, float scale, float* out, const float* gate) {
-    return append_decode("mkv_append_decode", h, nullptr, layer, n, ntok, kn, v, tab, q, start, scale, out, gate);
+    return append_decode("mkv_append_decode", h, nullptr, layer, n, ntok, kn, v, tab, q, start, scale, out, false,
+                         gate);
+}
+
+int mkv_append_decode_g16(mkv_t* h, int layer, int n, int ntok, const float* kn, const float* v, const float* tab,
+                          const float* q, int start, float scale, uint16_t* out16, const float* gate) {
+    return append_decode("mkv_append_decode_g16", h, nullptr, layer, n, ntok, kn, v, tab, q, start, scale, out16, true,
+                         gate);
 }
 
 int mkv_append_decode_noalloc(mkv_t* h, int layer, int n, int ntok, const float* kn, const float* v,
@@ -390,7 +410,7 @@ int mkv_append_decode_noalloc(mkv_t* h, int layer, int n, int ntok, const float*
                     SCRATCH_CHUNKS, SCRATCH_FLOATS * sizeof(float));
     const DecodeWs ws{sp, SCRATCH_CHUNKS};
     return append_decode("mkv_append_decode_noalloc", h, &ws, layer, n, ntok, kn, v, tab, q, start, scale, out,
-                         gate);
+                         false, gate);
 }
 
 int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, float scale, float* out,
@@ -422,7 +442,9 @@ int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, fl
     }
     if (e == hipSuccess)
         e = traced(h, MKV_SPAN_MERGE,
-                   [&](const Launch& L) { return launch_merge(h->pws, rpk, T, n, start, span, nch, gate, out, L); });
+                   [&](const Launch& L) {
+                       return launch_merge(h->pws, rpk, T, n, start, span, nch, gate, out, false, L);
+                   });
     return e == hipSuccess ? MKV_OK : hip_fail(e, "mkv_prefill");
 }
 

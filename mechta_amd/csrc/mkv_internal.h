@@ -149,7 +149,7 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
                               float scale, const DecodePlan& p, const DecodeWs& ws, const FusedAppend& fa,
                               const Launch& L);
 hipError_t launch_decode_merge(int ntok, int n, int start, const DecodePlan& p, const DecodeWs& ws, const float* gate,
-                               float* out, const Launch& L);
+                               void* out, bool h16, const Launch& L);
 // Small prefill blocks on the f16 store (T < SMALL_PREFILL_MAX): the reference runs them through attn_fd4 (f32 Q,
 // exact f32 softmax; engine.rs:1237-1241), so they run on decode_f16's f32-class arithmetic, one column of work-groups
 // per block of 4 tokens over the decode's stages; partials [kvh][row < 32 nzb][nch][PART], then launch_merge.
@@ -163,9 +163,10 @@ size_t small_prefill_ws_floats(int T, int nch);
 hipError_t launch_small_prefill(const Geom& g, const void* base, int layer, const float* q, int T, int n, int start,
                                 float scale, const SmallPlan& p, float* ws, const Launch& L);
 // Merge of split-K partials laid out [kvh][row < rpk][chunk < nch][PART], row = token*8 + head of the kv head:
-// out[t][head] for t < ntok over the chunks (chunk_lo of span, nch) holding a key of [start, n + t), optional gate.
+// out[t][head] for t < ntok over the chunks (chunk_lo of span, nch) holding a key of [start, n + t), optional gate;
+// out is f32, or with h16 f16 bits rounded to nearest even (attn_gate16).
 hipError_t launch_merge(const float* part, int rpk, int ntok, int n, int start, int span, int nch, const float* gate,
-                        float* out, const Launch& L);
+                        void* out, bool h16, const Launch& L);
 // q/k producer (rmsnorm of the q and k heads, rope2 of q) of ntok tokens; tab: [ntok][64] device RoPE rows.
 hipError_t launch_qk_produce(int ntok, const float* qf, const float* kb, const float* q_w, const float* k_w,
                              float eps, const float* tab, float* q_out, float* kn_out, const Launch& L);

@@ -546,6 +546,19 @@ void orc_gate(const float* att, const float* qf, int ntok, float* out) {
         }
 }
 
+/* attn_gate16 (ops.wgsl:296-300): the same product, a[i] * sigm(b[h*512 + 256 + d]), written as f16 pairs by
+ * pack2x16float (round to nearest even); the 4-token verify (quad.rs:125) and the f16-activation 2-token step
+ * (engine.rs:1103) write their gated attention this way. */
+void orc_gate16(const float* att, const float* qf, int ntok, uint16_t* out) {
+    for (int t = 0; t < ntok; t++)
+        for (int i = 0; i < ORC_H * ORC_D; i++) {
+            int h = i / ORC_D, d = i % ORC_D;
+            float g = qf[(size_t)t * ORC_H * 512 + (size_t)h * 512 + 256 + d];
+            float s = 1.0f / (1.0f + expf(-g));
+            out[(size_t)t * ORC_H * ORC_D + i] = orc_f32_to_f16(att[(size_t)t * ORC_H * ORC_D + i] * s);
+        }
+}
+
 /* rmsnorm (ops.wgsl:27-57) for rows of 256 values, as the q/k norms call it (uniforms qn / kn, quad.rs:50;
  * engine.rs:965, :1182; f1 = 1, flag = 1: weight, no gate): one work-group of 256 threads per row, thread t holds
  * x[t]^2, then the shared-memory tree partial[t] += partial[t + m] for m = 128, 64, .., 1; scale = 1 / sqrt(sum / n +

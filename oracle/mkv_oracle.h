@@ -77,6 +77,7 @@ void orc_attn_fd4(int fmt, const void* kc, const void* vc, const float* q, int T
 
 /* Output gate, attn_gate (ops.wgsl:171-177): out[t][h*256+d] = att[t][h*256+d] * sigmoid(qf[t][h*512+256+d]). */
 void orc_gate(const float* att, const float* qf, int ntok, float* out);
+void orc_gate16(const float* att, const float* qf, int ntok, uint16_t* out);
 
 /* Threads used by the OpenMP loops (for the CPU-baseline report). */
 int orc_threads(void);

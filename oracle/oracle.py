@@ -39,6 +39,7 @@ def lib():
         _lib.orc_attn_fa_f32.argtypes = [P, P, P, I, I, I, F, P, I, P]
         _lib.orc_attn_fd4.argtypes = [I, P, P, P, I, I, F, I, P]
         _lib.orc_gate.argtypes = [P, P, I, P]
+        _lib.orc_gate16.argtypes = [P, P, I, P]
         _lib.orc_rmsnorm_rows.argtypes = [P, I, I, P, F, P]
         _lib.orc_qk_norm_rope.argtypes = [P, P, I, P, P, F, P, P, P]
         _lib.orc_threads.restype = I
@@ -155,6 +156,16 @@ def gate(att, qf):
     qf = _c(qf, np.float32).reshape(ntok, H * 512)
     out = np.empty_like(att)
     lib().orc_gate(_p(att), _p(qf), ntok, _p(out))
+    return out
+
+
+def gate16(att, qf):
+    """attn_gate16: the gated attention as f16 bits (uint16), rounded to nearest even."""
+    att = _c(att, np.float32).reshape(-1, H * D)
+    ntok = att.shape[0]
+    qf = _c(qf, np.float32).reshape(ntok, H * 512)
+    out = np.empty(att.shape, np.uint16)
+    lib().orc_gate16(_p(att), _p(qf), ntok, _p(out))
     return out
 
 

@@ -19,7 +19,7 @@ HEADER = os.path.join(ROOT, "include", "mechta_kv.h")
 def declared_symbols():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"\b(mkv_[a-z_]+)\s*\(", src)))
+    return sorted(set(re.findall(r"\b(mkv_[a-z0-9_]+)\s*\(", src)))
 
 
 def test_library_exports_every_declared_symbol():

@@ -29,7 +29,7 @@ def rng(seed):
 
 def test_flint_symbols_exported():
     src = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
-    names = sorted(set(re.findall(r"\b(mfl_[a-z_]+)\s*\(", src)))
+    names = sorted(set(re.findall(r"\b(mfl_[a-z0-9_]+)\s*\(", src)))
     assert sorted(mf.SYMBOLS) == names
     L = mf.lib()
     for n in names:

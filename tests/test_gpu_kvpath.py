@@ -222,6 +222,40 @@ def test_decode_gate(torch_gpu, mk):
     assert_attn_close(out, ref, what="gated")
 
 
+@pytest.mark.parametrize("fmt,ctx,n0,ntok,start", [(F16, 4096, 777, 4, 0), (F16, 66560, 65537, 4, 0),
+                                                   (F16, 4096, 3000, 2, 0), (F16, 4096, 2000, 1, 500),
+                                                   (F32, 4096, 1500, 4, 0)])
+def test_gate16_output(torch_gpu, mk, fmt, ctx, n0, ntok, start):
+    """The gated attention as f16 (mkv_append_decode_g16 / mkv_decode_g16, the reference's attn_gate16 of the 4-token
+    verify, quad.rs:125, and of the f16 2-token step, engine.rs:1103): bit for bit the round-to-nearest-even f16 of
+    the f32 entry points' gated output, and within the attention bar of orc_gate16 over the oracle's attention."""
+    torch = torch_gpu
+    print(f"gate16 fmt={fmt} ctx={ctx} n0={n0} ntok={ntok} start={start}", flush=True)
+    kn, v = kv_inputs(41, ntok)
+    tab = O.rope_tables(n0 - 1, ntok)
+    q, qf = q_inputs(42, ntok), gate_inputs(43, ntok)
+    with mk.KvStore(1, ctx, fmt) as a, mk.KvStore(1, ctx, fmt) as b:
+        fill(torch, a, 0, fmt, n0 - 1, seed=44)
+        fill(torch, b, 0, fmt, n0 - 1, seed=44)
+        args = (0, n0, dev(torch, kn), dev(torch, v), dev(torch, tab), dev(torch, q))
+        h = a.append_decode(*args, start=start, gate_src=dev(torch, qf), f16_out=True).cpu().numpy()
+        f = b.append_decode(*args, start=start, gate_src=dev(torch, qf)).cpu().numpy()
+        assert h.dtype == np.float16
+        assert np.array_equal(h.view(np.uint16), f.astype(np.float16).view(np.uint16))
+        h2 = a.decode(0, dev(torch, q), n0, start=start, gate_src=dev(torch, qf), f16_out=True).cpu().numpy()
+        assert np.array_equal(h2.view(np.uint16), h.view(np.uint16))
+        with pytest.raises(mk.MkvError):
+            a.decode(0, dev(torch, q), n0, start=start, f16_out=True)  # the f16 output is the gated one
+        kc, vc = caches_np(a, 0, n0 + ntok - 1) if ctx <= 8192 else (None, None)
+    if kc is not None:
+        if fmt == F32 or ntok == 1 or start > 0:
+            att = O.attn_fd(fmt, kc, vc, q, n0, start=start)
+        else:
+            att = O.attn_dmx(kc, vc, q, n0)
+        ref = O.gate16(att, qf).view(np.float16).astype(np.float32).reshape(h.shape)
+        assert_attn_close(h.astype(np.float32), ref, atol=2e-3, rtol=2e-3, what="gate16")
+
+
 @pytest.mark.parametrize("fmt", [F16, F32])
 @pytest.mark.parametrize("ctx,n0", [(4096, 1234), (4096, 1279), (4096, 1282), (4096, 66), (20480, 19199),
                                     (66560, 65536 + 63)])

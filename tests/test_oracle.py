@@ -21,6 +21,7 @@ Function -> what pins it:
                      -> v; identical keys -> mean of V; a key with a large score in a later tile (the running max
                      moves and the earlier tiles are shrunk).
   orc_gate           sigmoid closed form at 0 (x/2), large positive (x), large negative (0).
+  orc_gate16         numpy's float16 cast of orc_gate; ties to even, overflow to inf, subnormals.
 """
 import math
 
@@ -306,6 +307,22 @@ def test_gate_closed_form():
     assert np.allclose(O.gate(att, qf), 0.0, atol=1e-30)
     qf[:, :, :256] = 1e9  # the q half of qf is not read
     assert np.allclose(O.gate(att, qf), 0.0, atol=1e-30)
+
+
+def test_gate16_rounds_the_f32_gate_to_nearest_even():
+    """attn_gate16 (ops.wgsl:296-300) = pack2x16float of attn_gate's f32 product: numpy's float16 cast (round to
+    nearest even) of orc_gate's output, exact ties to even, overflow to infinity, subnormals kept."""
+    rng = np.random.default_rng(81)
+    att = rng.standard_normal((3, 16, 256), dtype=np.float32)
+    qf = rng.standard_normal((3, 16, 512), dtype=np.float32)
+    want = O.gate(att, qf).astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.gate16(att, qf), want)
+    # sigmoid(100) is 1 in f32, so the output is f16(att): ties and range edges
+    qf[:] = 100.0
+    att = np.zeros((1, 16, 256), np.float32)
+    att.flat[:6] = [1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -(1 + 2.0 ** -11), 70000.0, -70000.0, 2.0 ** -20]
+    got = O.gate16(att, qf[:1]).ravel()[:6]
+    assert list(got) == [0x3C00, 0x3C02, 0xBC00, 0x7C00, 0xFC00, 0x0010]
 
 
 # ---- q/k producer: rmsnorm (ops.wgsl:27-57) and rope2 (ops.wgsl:275-286) ----
