@@ -465,8 +465,8 @@ def test_decode_cfg1_full_size(torch_gpu, mk):
 
 def test_decode_cfg4_full_size(torch_gpu, mk):
     """the 10 full-attention layers at a 262,144-position context (5.37 GB of f16 K/V), a
-    4-token verify at positions 262,140..262,143 on every layer (append through the fused entry); layers 0, 5 and 9
-    against the oracle, every layer finite; then 2 drafts rolled back and layer 0 re-verified over them."""
+    4-token verify at positions 262,140..262,143 on every layer (append through the fused entry), every layer against
+    the oracle; then 2 drafts rolled back and layer 0 re-verified over them."""
     torch = torch_gpu
     print("decode cfg4 full size", flush=True)
     L, ctx = 10, 262144
@@ -480,7 +480,8 @@ def test_decode_cfg4_full_size(torch_gpu, mk):
         outs = [st.append_decode(layer, pos + 1, dev(torch, kn), dev(torch, v), tab, dev(torch, q)).cpu().numpy()
                 for layer in range(L)]
         assert all(np.isfinite(o).all() for o in outs)
-        for layer in (0, 5, 9):
+        for layer in range(L):
+            print(f"cfg4 layer {layer} vs the oracle", flush=True)
             kc, vc = caches_np(st, layer, pos + 4)
             assert_attn_close(outs[layer], O.attn_dmx(kc, vc, q, pos + 1), what=f"cfg4 layer {layer}")
         st.set_len(pos + 2)
