@@ -324,19 +324,23 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
     // below are its own copies (K's are in either layout).
     const unsigned kreg = w * (TB / PF_NW);
     const unsigned vreg0 = FMT == 1 ? (2 * (w >> 1)) * (HD * 16) + (w & 1) * (HD / 2 * 16) : kreg;
+    // per-lane offsets of the wave's regions, fixed for the kernel; the tile's base and LDS slot are wave-uniform
+    const unsigned vk = kreg + lane * 16, vv = vreg0 + lane * 16;
+    const unsigned lk = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void*)ring + kreg);
+    const unsigned lv = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void*)ring + vreg0);
     auto issue = [&](int j) {
-        unsigned char* dst = ring + (j % PF_NSLOT) * SLOT;
+        const unsigned slot = (j % PF_NSLOT) * SLOT;
 #pragma unroll
         for (int u = 0; u < SUB; u++) {
             // a 32-position tile is one 32-row block of the ring (rows are a multiple of 32), K and V alike; tiles
             // past the split's end stay inside the plane and are never computed
-            const size_t off = (size_t)((lo + TILE * (SUB * j + u)) % rows) * HD * Gm::BPE + lane * 16;
+            const size_t off = (size_t)((lo + TILE * (SUB * j + u)) % rows) * HD * Gm::BPE;
 #pragma unroll
             for (int d = 0; d < Gm::DPT; d++) {
-                dma16(K + off + kreg + d * 1024, dst + u * TB + kreg + d * 1024);
+                dma16s(K + off + d * 1024, vk, lk + slot + u * TB + d * 1024);
                 // f32: d = 0, 1 are the two groups' 1 KB (DPT = 2); f16: the wave's 1 KB parts in order
-                const unsigned vo = FMT == 1 ? vreg0 + d * (HD * 16) : vreg0 + d * 1024;
-                dma16(V + off + vo, dst + (SUB + u) * TB + vo);
+                const unsigned vd = FMT == 1 ? d * (HD * 16) : d * 1024;
+                dma16s(V + off + vd, vv, lv + slot + (SUB + u) * TB + vd);
             }
         }
     };

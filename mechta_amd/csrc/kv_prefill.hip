@@ -81,18 +81,19 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
     __shared__ __attribute__((aligned(16))) unsigned char ring[NSLOT * SLOT_BYTES];
     __shared__ __attribute__((aligned(16))) float cfs[NW][32];  // rescale factors of a wave's rows
     const int ntiles = (ce - cs + 32 * SUB - 1) / (32 * SUB);
+    constexpr int PART_BYTES = SUB * TILE_BYTES / NW;
+    // the wave's part of a tile: a per-lane offset fixed for the kernel; the tile's base and LDS slot are wave-uniform
+    const unsigned voff = w * PART_BYTES + lane * 16;
+    const unsigned wlds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void*)ring + w * PART_BYTES);
     auto issue = [&](int j) {  // each wave copies 1/NW of tile j's K blocks and V groups into slot j % NSLOT
-        constexpr int PART_BYTES = SUB * TILE_BYTES / NW;
         const int k0 = cs + 32 * SUB * j;
-        const unsigned char* ks =
-            (const unsigned char*)(K + (size_t)(k0 / KBLK) * (KBLK * HD)) + w * PART_BYTES + lane * 16;
-        const unsigned char* vs =
-            (const unsigned char*)(V + (size_t)(k0 / VGRP) * (VGRP * HD)) + w * PART_BYTES + lane * 16;
-        unsigned char* dst = ring + (j % NSLOT) * SLOT_BYTES + w * PART_BYTES;
+        const unsigned char* ks = (const unsigned char*)(K + (size_t)(k0 / KBLK) * (KBLK * HD));
+        const unsigned char* vs = (const unsigned char*)(V + (size_t)(k0 / VGRP) * (VGRP * HD));
+        const unsigned dst = wlds + (j % NSLOT) * SLOT_BYTES;
 #pragma unroll
-        for (int i = 0; i < PART_BYTES / 1024; i++) dma16(ks + i * 1024, dst + i * 1024);
+        for (int i = 0; i < PART_BYTES / 1024; i++) dma16s(ks + i * 1024, voff, dst + i * 1024);
 #pragma unroll
-        for (int i = 0; i < PART_BYTES / 1024; i++) dma16(vs + i * 1024, dst + SUB * TILE_BYTES + i * 1024);
+        for (int i = 0; i < PART_BYTES / 1024; i++) dma16s(vs + i * 1024, voff, dst + SUB * TILE_BYTES + i * 1024);
     };
     for (int j = 0; j < NSLOT - 1 && j < ntiles; j++) issue(j);
 
@@ -312,16 +313,21 @@ __global__ void __launch_bounds__(P32_NW * 64) prefill_f32(const float* __restri
     // [128 (w % 2), +128) of groups 2 (w / 2) and 2 (w / 2) + 1 (2 KB each).
     const unsigned kreg = w * (P32_TILE / P32_NW);
     const unsigned vreg0 = (2 * (w >> 1)) * (HD * 16) + (w & 1) * (HD / 2 * 16), vreg1 = vreg0 + HD * 16;
+    static_assert(P32_TILE / P32_NW == 4096 && HD / 2 * 16 == 2048, "4 KB of K and 2 x 2 KB of V per wave");
+    // per-lane offsets of the wave's regions, fixed for the kernel; the tile's base and LDS slot are wave-uniform
+    const unsigned vk = kreg + lane * 16, v0 = vreg0 + lane * 16, v1 = vreg1 + lane * 16;
+    const unsigned lk = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void*)ring + kreg);
+    const unsigned l0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void*)ring + P32_TILE + vreg0);
+    const unsigned l1 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void*)ring + P32_TILE + vreg1);
     auto issue = [&](int j) {
         const size_t off = (size_t)(cs + 32 * j) * HD * 4;
-        unsigned char* dst = ring + (j & 1) * P32_SLOT;
-        static_assert(P32_TILE / P32_NW == 4096 && HD / 2 * 16 == 2048, "4 KB of K and 2 x 2 KB of V per wave");
+        const unsigned slot = (j & 1) * P32_SLOT;
 #pragma unroll
-        for (int d = 0; d < 4; d++) dma16(K + off + kreg + d * 1024 + lane * 16, dst + kreg + d * 1024);
+        for (int d = 0; d < 4; d++) dma16s(K + off + d * 1024, vk, lk + slot + d * 1024);
 #pragma unroll
         for (int d = 0; d < 2; d++) {
-            dma16(V + off + vreg0 + d * 1024 + lane * 16, dst + P32_TILE + vreg0 + d * 1024);
-            dma16(V + off + vreg1 + d * 1024 + lane * 16, dst + P32_TILE + vreg1 + d * 1024);
+            dma16s(V + off + d * 1024, v0, l0 + slot + d * 1024);
+            dma16s(V + off + d * 1024, v1, l1 + slot + d * 1024);
         }
     };
     if (ntiles > 0) issue(0);

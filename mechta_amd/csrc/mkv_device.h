@@ -121,5 +121,12 @@ __device__ inline void dma16(const void* src, void* lds_base) {
     const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void*)lds_base);  // wave-uniform
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
+// The same load with a wave-uniform 64-bit base in scalar registers and a 32-bit per-lane byte offset (the
+// instruction's saddr form): lane i's 16 bytes from sbase + voff land at lds + 16i. With the base and the LDS address
+// computed on the scalar unit, issuing a tile's loads takes no vector instruction.
+__device__ inline void dma16s(const void* sbase, unsigned voff, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+                 : "memory", "m0");
+}
 
 }  // namespace mkv
