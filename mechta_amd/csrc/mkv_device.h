@@ -125,7 +125,14 @@ __device__ inline void dma16(const void* src, void* lds_base) {
 // instruction's saddr form): lane i's 16 bytes from sbase + voff land at lds + 16i. With the base and the LDS address
 // computed on the scalar unit, issuing a tile's loads takes no vector instruction.
 __device__ inline void dma16s(const void* sbase, unsigned voff, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+    // both halves of the base through readfirstlane: scalar registers whatever the compiler proved (free when it did);
+    // readfirstlane returns int, so each half widens through unsigned (no sign extension into the high word)
+    const unsigned long long a = (unsigned long long)(uintptr_t)sbase;
+    const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+    const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)a);
+    const unsigned long long b = (unsigned long long)hi << 32 | lo;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(b),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
                  : "memory", "m0");
 }
 
