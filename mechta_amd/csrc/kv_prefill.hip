@@ -57,6 +57,28 @@ __device__ inline void wait_tiles(int later) {  // at most `later` tiles (LPT di
     }
 }
 
+// Maxima of the softmax on scores that are never NaN (masked scores are -inf), as single instructions: fmaxf's NaN
+// handling would add a canonicalizing max per operand.
+__device__ inline float vmax(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ inline float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+// The maximum over lanes l and l ^ 32, in every lane: v_permlane32_swap of two registers that both hold x leaves one
+// half's values in both halves of one register and the other half's in the other (the copy makes them two registers:
+// with one register the swap would exchange a register's halves with themselves).
+__device__ inline float max_xor32(float x) {
+    float y;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restrict__ kplane,
                                                    const _Float16* __restrict__ vplane, size_t plane_elems,
                                                    const float* __restrict__ q, int T, int n, int start, float scale2,
@@ -115,6 +137,14 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
         }
     }
     const int kaddr = h * 512 + key_perm(r) * 16;
+    // the smallest window end of each row block (its first token's; 0 when the block runs past T): a tile with every
+    // key below it, and none below start, needs no mask (a wave-uniform test)
+    int vmin[RB];
+#pragma unroll
+    for (int b = 0; b < RB; b++) {
+        const int tf = __builtin_amdgcn_readfirstlane(t0 + 4 * b);
+        vmin[b] = tf + 3 < T ? n + tf : 0;
+    }
     float m[RB], lsum[RB];
     f32x16 O[RB][8];
 #pragma unroll
@@ -163,17 +193,17 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
         for (int b = 0; b < RB; b++) {
             // the causal / start mask only where this tile crosses a row's window (raw scores; the scale, log2
             // units, is applied to the max and inside the exponent's FMA)
-            if (!__all(k0 >= start && k0 + 32 <= vis[b])) {
+            if (!(k0 >= start && k0 + 32 <= vmin[b])) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int key = k0 + 8 * h + i + (i >= 8 ? 8 : 0);
                     Scur[b][i] = (key < vis[b] && key >= start) ? Scur[b][i] : NEG_INF;
                 }
             }
-            float mt = Scur[b][0];
+            float mt = vmax(Scur[b][0], Scur[b][1]);
 #pragma unroll
-            for (int i = 1; i < 16; i++) mt = fmaxf(mt, Scur[b][i]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            for (int i = 2; i < 16; i += 2) mt = vmax3(mt, Scur[b][i], Scur[b][i + 1]);
+            mt = max_xor32(mt);
             mt *= scale2;  // scale2 > 0: the max of the scaled scores is the scaled max
             // the reference max moves when first or when the tile max exceeds it by more than 8; O and the sum are
             // rescaled only when a finite reference moved (rare: the exponential is not evaluated otherwise)
@@ -200,11 +230,11 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             // P = 2^(s * scale2 - m) (one FMA): masked scores are -inf and give 0 (the reference is 0 while a row has seen no key);
             // the row sum takes the f32 P, as attn_fa_mx does, the P.V operand its f16 rounding
             const float base = mr == NEG_INF ? 0.f : mr;
-            float ls = 0.f;
+            float ls;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const float p = fast_exp2(__builtin_fmaf(Scur[b][i], scale2, -base));
-                ls += p;
+                ls = i == 0 ? p : ls + p;  // 0 + p0 is p0: the same sum without the first add
                 pa[b][i >> 3][i & 7] = (_Float16)p;
             }
             lsum[b] = lsum[b] * cf + ls;
