@@ -31,8 +31,10 @@ constexpr int TILE = 32;                       // keys per tile: one K block, ei
 constexpr unsigned TILE_BYTES = TILE * HD * 4;  // 32 KB of each plane
 constexpr int QPAD = HD + 8;                   // LDS row of Q's halves: 16-byte reads of 32 rows conflict-free
 
-__device__ inline f32x4 bload4f(rsrc_t r, unsigned off) {
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, LOAD_NT));
+// voff: the lane's offset (fixed for the kernel), soff: the wave-uniform tile offset in the scalar operand (no vector
+// instruction per load for the tile base)
+__device__ inline f32x4 bload4f(rsrc_t r, unsigned voff, unsigned soff) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, LOAD_NT));
 }
 
 struct Tile {
@@ -84,12 +86,12 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
     const unsigned kofs = ((16 * w + 2 * s) * TILE + r32) * 16;  // + (4k + e) * 512 B: dims 64w + 16k + 8s + 4e
     const unsigned vofs = (s * HD + 64 * w + r32) * 16;            // + (4k + 2e) * 4 KB + c * 32 dims * 16 B
     auto load = [&](Tile& X, int j) {
-        const unsigned base = (unsigned)(j * tstep) * TILE_BYTES;
+        const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(j * tstep) * TILE_BYTES);
 #pragma unroll
-        for (int i = 0; i < 8; i++) X.k[i] = bload4f(kr, base + kofs + ((i >> 1) * 4 + (i & 1)) * (TILE * 16));
+        for (int i = 0; i < 8; i++) X.k[i] = bload4f(kr, kofs + ((i >> 1) * 4 + (i & 1)) * (TILE * 16), base);
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            X.v[i] = bload4f(vr, base + vofs + ((i >> 2) * 4 + 2 * (i & 1)) * (HD * 16) + ((i >> 1) & 1) * (32 * 16));
+            X.v[i] = bload4f(vr, vofs + ((i >> 2) * 4 + 2 * (i & 1)) * (HD * 16) + ((i >> 1) & 1) * (32 * 16), base);
     };
 
     // Q's loads, then the first two tiles': loads complete in order, so the Q split below waits for Q only, and the
@@ -184,7 +186,6 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
         // exact-max online softmax in log2 units on the raw scores (scale2 > 0: the max of the scaled scores is the
         // scaled max, and the exponent is one FMA); masked scores are -inf. A tile that lies inside every row's window
         // (the common case) takes no mask.
-        float mt = NEG_INF;
         if (!(k0 >= start && k0 + TILE <= n + t0 && k0 + TILE <= hi)) {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
@@ -192,9 +193,11 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
                 sv[i] = (key >= start && key < vis && key < hi) ? sv[i] : NEG_INF;
             }
         }
+        // scores here are never NaN (keys of stale rows are masked above): single-instruction maxima
+        float mt = vmax(sv[0], sv[1]);
 #pragma unroll
-        for (int i = 0; i < 16; i++) mt = fmaxf(mt, sv[i]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32)) * scale2;
+        for (int i = 2; i < 16; i += 2) mt = vmax3(mt, sv[i], sv[i + 1]);
+        mt = max_xor32(mt) * scale2;
         const float mn = fmaxf(m_run, mt);
         const float base = mn == NEG_INF ? 0.f : mn;
         const float cf = m_run == NEG_INF ? 0.f : fast_exp2(m_run - mn);
@@ -204,7 +207,7 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
             sv[i] = fast_exp2(__builtin_fmaf(sv[i], scale2, -base));
             ls += sv[i];
         }
-        ls += __shfl_xor(ls, 32);
+        ls = add_xor32(ls);
         l_run = l_run * cf + ls;
         m_run = mn;
         // rescale O: register i of this lane holds row 8(i/4) + 4s + i%4; the rows' factors pass through this wave's

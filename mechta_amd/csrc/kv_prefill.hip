@@ -57,28 +57,6 @@ __device__ inline void wait_tiles(int later) {  // at most `later` tiles (LPT di
     }
 }
 
-// Maxima of the softmax on scores that are never NaN (masked scores are -inf), as single instructions: fmaxf's NaN
-// handling would add a canonicalizing max per operand.
-__device__ inline float vmax(float a, float b) {
-    float r;
-    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
-__device__ inline float vmax3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-// The maximum over lanes l and l ^ 32, in every lane: v_permlane32_swap of two registers that both hold x leaves one
-// half's values in both halves of one register and the other half's in the other (the copy makes them two registers:
-// with one register the swap would exchange a register's halves with themselves).
-__device__ inline float max_xor32(float x) {
-    float y;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-    return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
 __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restrict__ kplane,
                                                    const _Float16* __restrict__ vplane, size_t plane_elems,
                                                    const float* __restrict__ q, int T, int n, int start, float scale2,
