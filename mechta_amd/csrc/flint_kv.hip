@@ -158,14 +158,15 @@ __global__ void __launch_bounds__(256) fl_attn(const void* __restrict__ kplane, 
 #pragma unroll
             for (int b = 0; b < 4; b++) sv[4 * a + b] = (p0[b] + p1[b]) + (p2[b] + p3[b]);
         }
-        float mt = NEG_INF;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int key = k0 + 8 * (i >> 2) + 4 * s + (i & 3);
             sv[i] = (key >= plo && key <= prow && key < hi) ? sv[i] * scale2 : NEG_INF;
-            mt = fmaxf(mt, sv[i]);
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        float mt = vmax(sv[0], sv[1]);  // masked scores are -inf, never NaN: single-instruction maxima
+#pragma unroll
+        for (int i = 2; i < 16; i += 2) mt = vmax3(mt, sv[i], sv[i + 1]);
+        mt = max_xor32(mt);
         const float mn = fmaxf(m_run, mt);
         const float base = mn == NEG_INF ? 0.f : mn;
         const float cf = m_run == NEG_INF ? 0.f : fast_exp2(m_run - mn);
@@ -175,7 +176,7 @@ __global__ void __launch_bounds__(256) fl_attn(const void* __restrict__ kplane, 
             sv[i] = fast_exp2(sv[i] - base);
             ls += sv[i];
         }
-        ls += __shfl_xor(ls, 32);
+        ls = add_xor32(ls);
         l_run = l_run * cf + ls;
         m_run = mn;
         if (__builtin_amdgcn_ballot_w64(cf != 1.f)) {
@@ -480,10 +481,10 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
                     S[i] = (key >= vlo && key < vhi) ? S[i] : NEG_INF;
                 }
             }
-            float mt = S[0];
+            float mt = vmax(S[0], S[1]);  // masked scores are -inf, never NaN: single-instruction maxima
 #pragma unroll
-            for (int i = 1; i < 16; i++) mt = fmaxf(mt, S[i]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            for (int i = 2; i < 16; i += 2) mt = vmax3(mt, S[i], S[i + 1]);
+            mt = max_xor32(mt);
             mt *= scale2;  // scale2 > 0: the max of the scaled scores is the scaled max
             const bool rescale = m != NEG_INF && mt > m + LAZY2;
             const float mr = m == NEG_INF || rescale ? fmaxf(m, mt) : m;
@@ -800,15 +801,14 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
             }
         }
         float sv[4];
-        float mt = NEG_INF;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int key = k0 + 4 * g + r;
             sv[r] = (key >= plo && key <= prow && key < hi) ? S[r] * scale2 : NEG_INF;
-            mt = fmaxf(mt, sv[r]);
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        float mt = vmax3(vmax(sv[0], sv[1]), sv[2], sv[3]);  // masked scores are -inf, never NaN
+        mt = vmax(mt, __shfl_xor(mt, 16));
+        mt = max_xor32(mt);
         const float mn = fmaxf(m_run, mt);
         const float base = mn == NEG_INF ? 0.f : mn;
         const float cf = m_run == NEG_INF ? 0.f : fast_exp2(m_run - mn);
@@ -819,7 +819,7 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
             ls += sv[r];
         }
         ls += __shfl_xor(ls, 16);
-        ls += __shfl_xor(ls, 32);
+        ls = add_xor32(ls);
         l_run = l_run * cf + ls;
         m_run = mn;
         if (__builtin_amdgcn_ballot_w64(cf != 1.f)) {  // register r of O holds row 4g + r

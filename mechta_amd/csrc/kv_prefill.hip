@@ -432,10 +432,10 @@ __global__ void __launch_bounds__(P32_NW * 64) prefill_f32(const float* __restri
                 S[i] = (key >= start && key < vis) ? S[i] : NEG_INF;
             }
         }
-        float mt = S[0];
+        float mt = vmax(S[0], S[1]);  // masked scores are -inf, never NaN: single-instruction maxima
 #pragma unroll
-        for (int i = 1; i < 16; i++) mt = fmaxf(mt, S[i]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        for (int i = 2; i < 16; i += 2) mt = vmax3(mt, S[i], S[i + 1]);
+        mt = max_xor32(mt);
         mt *= scale2;  // scale2 > 0
         const bool rescale = m != NEG_INF && mt > m + LAZY2;
         const float mr = m == NEG_INF || rescale ? fmaxf(m, mt) : m;
