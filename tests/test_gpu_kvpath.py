@@ -466,7 +466,7 @@ def test_decode_cfg1_full_size(torch_gpu, mk):
 def test_decode_cfg4_full_size(torch_gpu, mk):
     """the 10 full-attention layers at a 262,144-position context (5.37 GB of f16 K/V), a
     4-token verify at positions 262,140..262,143 on every layer (append through the fused entry), every layer against
-    the oracle; then 2 drafts rolled back and layer 0 re-verified over them."""
+    the oracle, a windowed 64-token prefill on the last layer; then 2 drafts rolled back and layer 0 re-verified."""
     torch = torch_gpu
     print("decode cfg4 full size", flush=True)
     L, ctx = 10, 262144
@@ -484,6 +484,14 @@ def test_decode_cfg4_full_size(torch_gpu, mk):
             print(f"cfg4 layer {layer} vs the oracle", flush=True)
             kc, vc = caches_np(st, layer, pos + 4)
             assert_attn_close(outs[layer], O.attn_dmx(kc, vc, q, pos + 1), what=f"cfg4 layer {layer}")
+        # a 64-token prefill block at the end of the last layer, over a 2,048-position window: its tiles lie more
+        # than 5 GB into the store, where tile addresses have low words at and above 2^31 (the prefill kernels take
+        # the tile base as a 64-bit scalar)
+        T, n = 64, pos + 4 - 64 + 1
+        q64 = q_inputs(985, T) / 4
+        out = st.prefill(L - 1, dev(torch, q64), n, start=n - 2048).cpu().numpy()
+        ref, atol, rtol = prefill_reference(F16, kc, vc, q64, n, start=n - 2048)
+        assert_attn_close(out, ref, atol=atol, rtol=rtol, what="cfg4 last layer, 64-token prefill")
         st.set_len(pos + 2)
         kn2, v2 = kv_inputs(983, 2)
         q2 = q_inputs(984, 2)
