@@ -481,7 +481,9 @@ __global__ void __launch_bounds__(PF_NW * 64) fl_pf(const void* __restrict__ kpl
                     S[i] = (key >= vlo && key < vhi) ? S[i] : NEG_INF;
                 }
             }
-            float mt = vmax(S[0], S[1]);  // masked scores are -inf, never NaN: single-instruction maxima
+            // masked scores are -inf, never NaN: single-instruction maxima after the first, which is the compiler's
+            // (it reads the MFMA results and so carries the wait states a vector read of them needs)
+            float mt = fmaxf(S[0], S[1]);
 #pragma unroll
             for (int i = 2; i < 16; i += 2) mt = vmax3(mt, S[i], S[i + 1]);
             mt = max_xor32(mt);

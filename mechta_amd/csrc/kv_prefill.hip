@@ -178,7 +178,9 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
                     Scur[b][i] = (key < vis[b] && key >= start) ? Scur[b][i] : NEG_INF;
                 }
             }
-            float mt = vmax(Scur[b][0], Scur[b][1]);
+            // the first maximum is the compiler's: it reads the MFMA results and so carries the wait states a
+            // vector read of them needs, which inline assembly would not get; the rest follows it
+            float mt = fmaxf(Scur[b][0], Scur[b][1]);
 #pragma unroll
             for (int i = 2; i < 16; i += 2) mt = vmax3(mt, Scur[b][i], Scur[b][i + 1]);
             mt = max_xor32(mt);

@@ -138,7 +138,9 @@ __device__ inline void dma16s(const void* sbase, unsigned voff, unsigned lds) {
 
 
 // Maxima of the softmax on scores that are never NaN (masked scores are -inf), as single instructions: fmaxf's NaN
-// handling would add a canonicalizing max per operand.
+// handling would add a canonicalizing max per operand. Inline assembly gets no hazard wait states from the compiler:
+// its operands must not be MFMA results read directly (a vector read of those needs wait states the compiler inserts
+// only before its own instructions), so a chain over accumulators starts with a compiler maximum.
 __device__ inline float vmax(float a, float b) {
     float r;
     asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
