@@ -27,24 +27,40 @@ __device__ inline f32x4 mfma16(half8 a, half8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// f32 products on the f16 matrix units. An f32 operand x is split into two f16 parts: hi = x with its 13 low mantissa
-// bits cleared (exact in f16 for |x| in f16's normal range) and lo = f16(x - hi) (the difference is exact in f32), so
-// |x - hi - lo| <= 2^-21 |x|; one AND, one subtraction and half a packed conversion per part and element (an f16
-// round trip for hi measured 4% slower). A product a.b is taken as hi(a)hi(b) + hi(a)lo(b) + lo(a)hi(b) with f32
-// accumulation; the dropped lo(a)lo(b) is below 2^-20 of |a||b|. Operands that are f16 already (an f16 cache's K or
-// V) need two passes.
-__device__ inline f32x4 trunc13(f32x4 x) {
-    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-    return __builtin_bit_cast(f32x4, __builtin_bit_cast(u32x4, x) & 0xFFFFE000u);
+// f32 products on the f16 matrix units. An f32 operand x is split into two f16 parts: hi = f16(x), rounded to nearest
+// even, and lo = f16(x - hi) (the difference is exact in f32), so |x - hi| <= 2^-11 |x| and |x - hi - lo| <= 2^-22 |x|
+// for |x| in f16's normal range. Per pair of elements: one packed conversion for hi, two v_fma_mix_f32 for x - hi (the
+// f16 hi read from its half of the packed register, so no conversion back to f32), one packed conversion for lo: two
+// vector instructions per element (clearing hi's low mantissa bits with an AND, then a subtraction, took three). A
+// product a.b is taken as hi(a)hi(b) + hi(a)lo(b) + lo(a)hi(b) with f32 accumulation; the dropped lo(a)lo(b) is below
+// 2^-22 of |a||b|. Operands that are f16 already (an f16 cache's K or V) need two passes. The inputs of a split are
+// never MFMA results read directly (inline assembly gets no hazard wait states from the compiler): they are loads, or
+// the softmax's vector results.
+template <bool HIGH>  // x - (float)(the f16 in the low or high half of pair)
+__device__ inline float sub_half(float x, unsigned pair) {
+    float d;
+    if constexpr (HIGH)
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(pair), "v"(x));
+    else
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(pair), "v"(x));
+    return d;
 }
-__device__ inline half8 f16x8(f32x4 a, f32x4 b) {
-    return half8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
-                 (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+__device__ inline void split2(float a, float b, unsigned& hi, unsigned& lo) {
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+    const half2v h = {(_Float16)a, (_Float16)b};
+    hi = __builtin_bit_cast(unsigned, h);
+    const half2v l = {(_Float16)sub_half<false>(a, hi), (_Float16)sub_half<true>(b, hi)};
+    lo = __builtin_bit_cast(unsigned, l);
 }
 __device__ inline void split8(f32x4 a, f32x4 b, half8& hi, half8& lo) {
-    const f32x4 ah = trunc13(a), bh = trunc13(b);
-    hi = f16x8(ah, bh);
-    lo = f16x8(a - ah, b - bh);
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    unsigned h0, h1, h2, h3, l0, l1, l2, l3;
+    split2(a.x, a.y, h0, l0);
+    split2(a.z, a.w, h1, l1);
+    split2(b.x, b.y, h2, l2);
+    split2(b.z, b.w, h3, l3);
+    hi = __builtin_bit_cast(half8, u32x4{h0, h1, h2, h3});
+    lo = __builtin_bit_cast(half8, u32x4{l0, l1, l2, l3});
 }
 // c += a.b with a = ah + al, b = bh + bl: three f16 MFMAs (al.bl dropped)
 __device__ inline f32x16 mfma3(half8 ah, half8 al, half8 bh, half8 bl, f32x16 c) {
@@ -52,11 +68,13 @@ __device__ inline f32x16 mfma3(half8 ah, half8 al, half8 bh, half8 bl, f32x16 c)
     c = mfma32(ah, bl, c);
     return mfma32(al, bh, c);
 }
-__device__ inline half4 f16x4(f32x4 a) { return half4{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w}; }
 __device__ inline void split4(f32x4 a, half4& hi, half4& lo) {
-    const f32x4 ah = trunc13(a);
-    hi = f16x4(ah);
-    lo = f16x4(a - ah);
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    unsigned h0, h1, l0, l1;
+    split2(a.x, a.y, h0, l0);
+    split2(a.z, a.w, h1, l1);
+    hi = __builtin_bit_cast(half4, u32x2{h0, h1});
+    lo = __builtin_bit_cast(half4, u32x2{l0, l1});
 }
 // c += a.(bh + bl) with a exact in f16: two passes
 __device__ inline f32x16 mfma2(half8 a, half8 bh, half8 bl, f32x16 c) { return mfma32(a, bl, mfma32(a, bh, c)); }
