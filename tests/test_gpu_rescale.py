@@ -3,7 +3,7 @@ exceeds it by more than 8, dmx.rs:72-74) moving in the middle of a split: with N
 so keys boosted 24x at a few positions force the rescale of O and of the row sums in decode_f16 and prefill_f16
 (and the exact-max rescale of the f32 kernels). Checked against the oracle's restatement of the matching reference
 kernel, at the task tolerance (f16 store) or within max-abs 1e-4 / relative 1e-5 (f32 store): with scores in the
-hundreds, an exp argument shifted by 2^-20 of the score (the split products' rounding) already moves an output by a
+hundreds, an exp argument shifted by 2^-22 of the score (the split products' rounding) already moves an output by a
 few 1e-5, so the f32 store's usual 1e-5 max-abs bar is relaxed here, and only here, to 1e-4.
 """
 import numpy as np
