@@ -142,6 +142,10 @@ __device__ inline void dma16(const void* src, void* lds_base) {
 // The same load with a wave-uniform 64-bit base in scalar registers and a 32-bit per-lane byte offset (the
 // instruction's saddr form): lane i's 16 bytes from sbase + voff land at lds + 16i. With the base and the LDS address
 // computed on the scalar unit, issuing a tile's loads takes no vector instruction.
+// Both helpers set m0, which the compiler reserves (hipcc warns about a reserved register in the clobber list): the
+// generated code of these kernels holds no value of its own in m0 (no LDS-DMA builtin, no s_sendmsg, no relative
+// VGPR indexing), so nothing live is overwritten. __builtin_amdgcn_global_load_lds manages m0 itself, but for these
+// loads it builds 64-bit per-lane addresses (8 more vector instructions per prefill_f16 tile and wave).
 __device__ inline void dma16s(const void* sbase, unsigned voff, unsigned lds) {
     // both halves of the base through readfirstlane: scalar registers whatever the compiler proved (free when it did);
     // readfirstlane returns int, so each half widens through unsigned (no sign extension into the high word)
