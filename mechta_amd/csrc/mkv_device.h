@@ -145,7 +145,8 @@ __device__ inline void dma16(const void* src, void* lds_base) {
 // Both helpers set m0, which the compiler reserves (hipcc warns about a reserved register in the clobber list): the
 // generated code of these kernels holds no value of its own in m0 (no LDS-DMA builtin, no s_sendmsg, no relative
 // VGPR indexing), so nothing live is overwritten. __builtin_amdgcn_global_load_lds manages m0 itself, but for these
-// loads it builds 64-bit per-lane addresses (8 more vector instructions per prefill_f16 tile and wave).
+// loads it builds 64-bit per-lane addresses (8 more vector instructions per prefill_f16 tile and wave): measured, the
+// cfg3 prefill fell from 43.7% to 42.0% of the f16 peak and the f32 prefill rose from 0.453 to 0.464 ms.
 __device__ inline void dma16s(const void* sbase, unsigned voff, unsigned lds) {
     // both halves of the base through readfirstlane: scalar registers whatever the compiler proved (free when it did);
     // readfirstlane returns int, so each half widens through unsigned (no sign extension into the high word)
