@@ -19,10 +19,11 @@ SOURCES = ["kv_store.cpp", "kv_root.cpp", "kv_append.hip", "kv_produce.hip", "kv
 # flint_kv: the same for the decodes' score accumulators, which the softmax reads every subtile (no accumulator-register
 # reads: f16 full-layer decode 20.4-20.5 against 20.8-20.9 us, sliding layer 10.3-10.4 against 10.6-10.7 us)
 # kv_prefill, kv_decode, kv_attn32: no NaN handling in fmaxf (masked scores are -inf, never NaN), so max reductions need no canonicalize
-# kv_prefill: the max-ilp machine scheduler (in alternating runs: prefill_f32 0.449 against 0.457-0.459 ms per
-# 512-token block, prefill_f16 42.6-42.8% against 42.5-42.6% of the f16 peak on one box)
+# kv_prefill, kv_decode: the max-ilp machine scheduler (in alternating runs: prefill_f32 0.449 against 0.457-0.459 ms
+# per 512-token block, prefill_f16 42.6-42.8% against 42.5-42.6% of the f16 peak on one box; cfg1 10.52-10.55 against
+# 10.63-10.68 us per step, the cfg2 decode unchanged)
 EXTRA = {"kv_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans", "-mllvm",
-                            "-amdgpu-sched-strategy=max-ilp"], "kv_decode.hip": ["-fno-honor-nans"],
+                            "-amdgpu-sched-strategy=max-ilp"], "kv_decode.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
          "kv_attn32.hip": ["-fno-honor-nans"], "flint_kv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"],
          "kv_produce.hip": ["-ffp-contract=off"]}
 # measurement aid of bench.py (a plain HBM read of a given size), its own library: not part of the KV-cache ABI
