@@ -120,3 +120,15 @@ def test_root_info_reads_the_reference_layout(tmp_path):
     with pytest.raises(mk.MkvError) as e:
         mk.root_info(tmp_path / "missing.bin")
     assert e.value.code == mk.E_IO
+
+
+def test_build_keeps_packed_fp32_off_for_every_source():
+    """Every HIP source is compiled with the packed-FP32 feature off (its v_pk_* f32 forms are not used on this
+    hardware), and no per-file flag set turns it back on."""
+    from mechta_amd import build as b
+    flags = b.FLAGS
+    i = flags.index("-target-feature")
+    assert flags[i - 1] == "-Xclang" and flags[i + 1] == "-Xclang" and flags[i + 2] == "-packed-fp32-ops"
+    for src, extra in b.EXTRA.items():
+        assert src in b.SOURCES, src
+        assert not any("packed-fp32" in x for x in extra), (src, extra)
