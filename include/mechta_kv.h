@@ -72,8 +72,13 @@ size_t mkv_buffer_bytes(int ctx, int fmt);
  * of slack past the last plane, the decode partials (2 kv heads x 32 rows x min(ctx / 64 + 2, 256) splits x 1,040
  * bytes) and the prefill partials (68,157,440 bytes: 2 kv heads x 4,096 (token, split) pairs x 8 heads x 1,040
  * bytes). 0 for arguments mkv_create refuses. The reference's memory check sizes the same cache as
- * 2 x layers x buffer_bytes_for(ctx) (memcheck.rs:110-111). */
+ * 2 x layers x buffer_bytes_for(ctx) (memcheck.rs:110-111). Not included: the no-allocation entry point's scratch
+ * (mkv_noalloc_scratch_bytes), a file-scope device array every GPU holds once the library is loaded, whatever the
+ * number of stores. */
 size_t mkv_store_bytes(int layers, int ctx, int fmt);
+/* Bytes of the device scratch of mkv_append_decode_noalloc, held on every GPU the library runs on until the process
+ * ends (16,506,880). No counterpart in the reference: for memory checks that must count it. */
+size_t mkv_noalloc_scratch_bytes(void);
 
 /* Allocates the store: layers x {K, V} x 2 heads x ctx x 256 elements, zero filled, and the split-K workspaces.
  * Replaces the per-layer KV buffer allocation (engine.rs:493-496) with the ctx check of check_ctx (engine.rs:28-33).
@@ -138,7 +143,11 @@ int mkv_append_decode_g16(mkv_t* h, int layer, int n, int ntok, const float* k_n
  * bit-identical to mkv_append_decode; the split-K partials go to a scratch array of the library (16,506,880 bytes per
  * GPU, held until the process ends) instead of the handle's workspace. Limit: at most 248 splits (every decode plan of
  * 1..4 tokens fits; MKV_E_SIZE otherwise, nothing enqueued). The scratch is shared by every handle on one GPU: calls
- * that overlap on one GPU (on different streams, or from different handles without ordering) race. */
+ * that overlap on one GPU (on different streams, or from different handles without ordering) race, so a caller with
+ * two handles on one GPU (e.g. the 10-layer store and the MTP layer's) must order their calls on one stream. The
+ * scratch's address is resolved by mkv_create with the device current (or by the first call, with the handle's device
+ * current); MKV_E_HIP when it cannot be. The handle's trace (mkv_trace) records nothing for this call: taking trace
+ * events may allocate. */
 int mkv_append_decode_noalloc(mkv_t* h, int layer, int n, int ntok, const float* k_normed, const float* v,
                               const float* rope_tab, const float* q, int start, float scale, float* out,
                               const float* gate_src);
@@ -153,7 +162,8 @@ int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, fl
 /* Prefix-cache snapshot of positions [0, p) of every layer (the KV part of read_root / write_root,
  * engine.rs:782-823). The byte image is the store's own layout, block-rounded; restore into a store of the same
  * layers / format (any ctx >= p) gives back bit-identical positions [0, p) and sets every layer's length to p.
- * host: pinned host memory (hipHostMalloc) of exactly mkv_snapshot_bytes(h, p) bytes.
+ * host: pinned host memory (hipHostMalloc) of exactly mkv_snapshot_bytes(h, p) bytes; pageable memory is refused with
+ * MKV_E_ARG before anything is enqueued.
  * mkv_snapshot waits until the copy has landed in host memory; mkv_restore returns when the copy is enqueued
  * (the host buffer must stay valid until mkv_sync). */
 size_t mkv_snapshot_bytes(const mkv_t* h, int p);
@@ -231,6 +241,24 @@ int mkv_root_wait(mkv_t* h);
 int mkv_root_info(const char* path, int* p, int* ns, int* nk, uint64_t* kv_words, uint64_t* ssm_words,
                   uint64_t* conv_words, int max_ns);
 int mkv_root_load(mkv_t* h, const char* path, uint32_t* tokens, float* const* ssm, float* const* conv);
+
+/* Root-file policy of the reference's session (session.rs:61-90):
+ * MKV_ROOT_MIN: a root is taken only for a system prompt of at least this many tokens (ROOT_MIN, session.rs:90).
+ * mkv_root_path: the file name of a root, "<dir>/root-<f16|f32>-<model key>-<token key>.bin" (root_file,
+ *   session.rs:68-73), the keys as 16 lower-case hex digits: the model key is FNV-1a 64 of the model path's bytes, each
+ *   byte taken as one u32 token (root_key over model_path().bytes().map(u32::from)), the token key mkv_root_key of the
+ *   prompt. Writes at most cap bytes with the terminating NUL; returns the name's length (not counting the NUL), or
+ *   MKV_E_ARG (NULL argument, bad format) / MKV_E_SIZE (cap too small, nothing written past out[cap - 1]).
+ * mkv_root_prune: keeps the `keep` (at least 1) most recently modified files of `dir` whose names start with
+ *   "root-<fmt>-" and end with ".bin", and removes the others (prune_roots, session.rs:75-84; MECHTA_ROOTS defaults to
+ *   6 there). Returns the number removed; 0 when the directory cannot be read (the reference gives up silently too).
+ * mkv_root_touch: sets a root file's modification time to now, so the pruning keeps it (touch, session.rs:86-88);
+ *   0, or MKV_E_IO when the file cannot be opened. */
+#define MKV_ROOT_MIN 2048
+int mkv_root_path(char* out, size_t cap, const char* dir, int fmt, const char* model_path, const uint32_t* tokens,
+                  size_t n);
+int mkv_root_prune(const char* dir, int fmt, int keep);
+int mkv_root_touch(const char* path);
 
 #ifdef __cplusplus
 }

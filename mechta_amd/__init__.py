@@ -25,7 +25,8 @@ SYMBOLS = ["mkv_create", "mkv_destroy", "mkv_set_stream", "mkv_sync", "mkv_last_
            "mkv_snapshot", "mkv_restore", "mkv_read_rows", "mkv_write_rows", "mkv_trace", "mkv_trace_read",
            "mkv_rope_table", "mkv_root_key", "mkv_root_save", "mkv_root_wait", "mkv_root_info", "mkv_root_load",
            "mkv_rope_table_dev", "mkv_qk_norm_rope", "mkv_buffer_bytes", "mkv_store_bytes",
-           "mkv_append_decode_noalloc", "mkv_decode_g16", "mkv_append_decode_g16"]
+           "mkv_append_decode_noalloc", "mkv_decode_g16", "mkv_append_decode_g16", "mkv_noalloc_scratch_bytes",
+           "mkv_root_path", "mkv_root_prune", "mkv_root_touch"]
 SPAN_KV_WRITE, SPAN_CORE, SPAN_MERGE = 0, 1, 2
 
 
@@ -81,6 +82,10 @@ def lib():
             "mkv_qk_norm_rope": ([P, I, I, P, P, P, P, F, P, P], I),
             "mkv_buffer_bytes": ([I, I], S),
             "mkv_store_bytes": ([I, I, I], S),
+            "mkv_noalloc_scratch_bytes": ([], S),
+            "mkv_root_path": ([ctypes.c_char_p, S, ctypes.c_char_p, I, ctypes.c_char_p, P, S], I),
+            "mkv_root_prune": ([ctypes.c_char_p, I, I], I),
+            "mkv_root_touch": ([ctypes.c_char_p], I),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -136,6 +141,33 @@ def root_key(tokens):
     import numpy as np
     t = np.ascontiguousarray(tokens, dtype=np.uint32)
     return lib().mkv_root_key(t.ctypes.data_as(ctypes.c_void_p), t.size)
+
+
+def root_path(dir, fmt, model_path, tokens):
+    """File name of a root (root_file, session.rs:68-73): <dir>/root-<f16|f32>-<model key>-<token key>.bin."""
+    import numpy as np
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    buf = ctypes.create_string_buffer(4096)
+    n = lib().mkv_root_path(buf, len(buf), os.fsencode(dir), fmt, os.fsencode(model_path),
+                            t.ctypes.data_as(ctypes.c_void_p), t.size)
+    _check(n if n < 0 else 0)
+    return os.fsdecode(buf.value)
+
+
+def root_prune(dir, fmt, keep=6):
+    """Keeps the `keep` most recently modified root files of the format in `dir` (prune_roots, session.rs:75-84);
+    returns how many it removed."""
+    n = lib().mkv_root_prune(os.fsencode(dir), fmt, keep)
+    _check(n if n < 0 else 0)
+    return n
+
+
+def root_touch(path):
+    """Marks a root file as just used (touch, session.rs:86-88)."""
+    _check(lib().mkv_root_touch(os.fsencode(path)))
+
+
+ROOT_MIN = 2048  # session.rs:90: a root only for a system prompt of at least this many tokens
 
 
 def root_info(path):

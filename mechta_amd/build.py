@@ -40,11 +40,27 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-ta
          "-I", os.path.join(HERE, "..", "include")]
 
 
+def _extra_flags():
+    """MKV_EXTRA_FLAGS: extra hipcc flags for development builds only. They are taken only with MKV_DEV_BUILD=1 set as
+    well (a warning is printed), and never when they name the packed-FP32 target feature, which every source keeps
+    off."""
+    extra = os.environ.get("MKV_EXTRA_FLAGS", "").split()
+    if not extra:
+        return []
+    if os.environ.get("MKV_DEV_BUILD") != "1":
+        raise RuntimeError("MKV_EXTRA_FLAGS is set without MKV_DEV_BUILD=1: refusing to build a library with "
+                           "unreviewed compiler flags")
+    if any("packed-fp32" in x for x in extra):
+        raise RuntimeError("MKV_EXTRA_FLAGS may not change the packed-FP32 target feature: " + " ".join(extra))
+    print("warning: development build with MKV_EXTRA_FLAGS = " + " ".join(extra), file=sys.stderr, flush=True)
+    return extra
+
+
 def _compile(src, verbose):
     obj = os.path.join(OUTDIR, "obj", os.path.splitext(src)[0] + ".o")
     os.makedirs(os.path.dirname(obj), exist_ok=True)
     lang = ["-x", "hip"]
-    cmd = [HIPCC] + FLAGS + EXTRA.get(src, []) + os.environ.get("MKV_EXTRA_FLAGS", "").split() + lang + ["-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC] + FLAGS + EXTRA.get(src, []) + _extra_flags() + lang + ["-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

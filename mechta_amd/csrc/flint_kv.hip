@@ -926,7 +926,9 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
             }
         }
         if (fused) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial's stores are complete
+            // release at agent scope (this wave stored the whole partial): the partial happens before the arrival
+            // that counts it; the kv head's last arrival then acquires, so its merge reads every partial
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
             int l = 0;
             if (lane == 0) {
                 l = __hip_atomic_fetch_add(arrivals + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -934,10 +936,11 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
                 if (l) __hip_atomic_store(arrivals + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 last = l;
             }
+            if (__builtin_amdgcn_readfirstlane(l)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         }
     }
     if (!fused) return;
-    __syncthreads();
+    __syncthreads();  // the other waves see the acquiring wave's view through the work-group barrier
     if (!last) return;
     // the kv head's last work-group: the merge of fl_merge for its rows (row = token * 8 + head of the kv head, T * 8
     // <= 16), thread = (row, 8 dims), every split's partial loaded in one round trip (device-coherent loads)

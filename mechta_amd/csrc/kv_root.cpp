@@ -9,6 +9,11 @@
 // The store keeps its own tiled layout; read_rows / write_rows (kv_append.hip) convert on the device.
 #include <hip/hip_runtime.h>
 
+#include <dirent.h>
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
@@ -304,4 +309,60 @@ int mkv_root_load(mkv_t* h, const char* path, uint32_t* tokens, float* const* ss
     }
     for (int l = 0; l < h->g.layers; l++) h->len[l] = p;
     return MKV_OK;
+}
+
+int mkv_root_path(char* out, size_t cap, const char* dir, int fmt, const char* model_path, const uint32_t* tokens,
+                  size_t n) {
+    if (!out || !dir || !model_path || (!tokens && n > 0)) return fail(MKV_E_ARG, "mkv_root_path: NULL argument");
+    if (fmt != MKV_F16 && fmt != MKV_F32) return fail(MKV_E_ARG, "mkv_root_path: format %d", fmt);
+    // the model key: every byte of the path is one token (root_key over the bytes widened to u32)
+    std::vector<uint32_t> mb;
+    for (const unsigned char* c = (const unsigned char*)model_path; *c; c++) mb.push_back(*c);
+    char name[64];
+    snprintf(name, sizeof name, "root-%s-%016llx-%016llx.bin", fmt == MKV_F16 ? "f16" : "f32",
+             (unsigned long long)mkv_root_key(mb.data(), mb.size()), (unsigned long long)mkv_root_key(tokens, n));
+    const std::string full = std::string(dir) + "/" + name;
+    if (full.size() + 1 > cap) return fail(MKV_E_SIZE, "mkv_root_path: %zu bytes needed, %zu given", full.size() + 1, cap);
+    memcpy(out, full.c_str(), full.size() + 1);
+    return (int)full.size();
+}
+
+int mkv_root_prune(const char* dir, int fmt, int keep) {
+    if (!dir || (fmt != MKV_F16 && fmt != MKV_F32)) return fail(MKV_E_ARG, "mkv_root_prune: bad argument");
+    keep = std::max(keep, 1);
+    const std::string prefix = std::string("root-") + (fmt == MKV_F16 ? "f16" : "f32") + "-";
+    DIR* d = opendir(dir);
+    if (!d) return 0;
+    struct Entry {
+        struct timespec mtime;
+        std::string path;
+    };
+    std::vector<Entry> v;
+    while (struct dirent* e = readdir(d)) {
+        const std::string name = e->d_name;
+        if (name.size() < prefix.size() + 4 || name.compare(0, prefix.size(), prefix) != 0 ||
+            name.compare(name.size() - 4, 4, ".bin") != 0)
+            continue;
+        const std::string path = std::string(dir) + "/" + name;
+        struct stat st;
+        if (stat(path.c_str(), &st) == 0) v.push_back({st.st_mtim, path});
+    }
+    closedir(d);
+    // newest first (the reference sorts by modification time, descending, and skips the first `keep`)
+    std::sort(v.begin(), v.end(), [](const Entry& a, const Entry& b) {
+        return a.mtime.tv_sec != b.mtime.tv_sec ? a.mtime.tv_sec > b.mtime.tv_sec : a.mtime.tv_nsec > b.mtime.tv_nsec;
+    });
+    int removed = 0;
+    for (size_t i = (size_t)keep; i < v.size(); i++)
+        if (unlink(v[i].path.c_str()) == 0) removed++;
+    return removed;
+}
+
+int mkv_root_touch(const char* path) {
+    if (!path) return fail(MKV_E_ARG, "mkv_root_touch: NULL path");
+    const int fd = open(path, O_WRONLY | O_APPEND);
+    if (fd < 0) return fail(MKV_E_IO, "mkv_root_touch: cannot open %s", path);
+    const int rc = futimens(fd, nullptr);  // both times to now
+    close(fd);
+    return rc == 0 ? MKV_OK : fail(MKV_E_IO, "mkv_root_touch: cannot set the time of %s", path);
 }

@@ -199,8 +199,10 @@ int mkv_create(mkv_t** out, int layers, int ctx, int fmt, void* stream) {
                     MKV_CTX_MAX);
     int dev = 0;
     hipError_t de = hipGetDevice(&dev);
-    if (de == hipSuccess) de = resolve_scratch(dev);
-    if (de != hipSuccess) return hip_fail(de, "mkv_create: scratch address of the current device");
+    if (de != hipSuccess) return hip_fail(de, "mkv_create: current device");
+    // the no-allocation entry point's scratch address on this device, resolved here while the device is current; a
+    // failure leaves that one entry point unavailable on the device (it then returns MKV_E_HIP), nothing else
+    (void)resolve_scratch(dev);
     mkv_store* h = new (std::nothrow) mkv_store;
     if (!h) return fail(MKV_E_NOMEM, "mkv_create: host allocation");
     h->device = dev;
@@ -401,6 +403,11 @@ int mkv_append_decode_noalloc(mkv_t* h, int layer, int n, int ntok, const float*
                               const float* gate) {
     if (!h) return fail(MKV_E_ARG, "mkv_append_decode_noalloc: NULL handle");
     float* sp = scratch_of(h->device);
+    if (!sp) {  // not resolved by mkv_create: once more, if the handle's device is the current one
+        int cur = -1;
+        if (hipGetDevice(&cur) == hipSuccess && cur == h->device && resolve_scratch(cur) == hipSuccess)
+            sp = scratch_of(cur);
+    }
     if (!sp) return fail(MKV_E_HIP, "mkv_append_decode_noalloc: no scratch address for device %d", h->device);
     // the split plan of this call, checked against the scratch's capacity before anything is enqueued
     const int nch = h->g.fmt == MKV_F32 ? attn32_plan(ntok < 1 ? 1 : ntok, n, start).nch
@@ -409,9 +416,16 @@ int mkv_append_decode_noalloc(mkv_t* h, int layer, int n, int ntok, const float*
         return fail(MKV_E_SIZE, "mkv_append_decode_noalloc: %d splits exceed the scratch's %d (%zu bytes)", nch,
                     SCRATCH_CHUNKS, SCRATCH_FLOATS * sizeof(float));
     const DecodeWs ws{sp, SCRATCH_CHUNKS};
-    return append_decode("mkv_append_decode_noalloc", h, &ws, layer, n, ntok, kn, v, tab, q, start, scale, out,
-                         false, gate);
+    // no trace events on this path: taking them may create events and grows the pending list (host allocations)
+    const bool tracing = h->tracing;
+    h->tracing = false;
+    const int rc = append_decode("mkv_append_decode_noalloc", h, &ws, layer, n, ntok, kn, v, tab, q, start, scale,
+                                 out, false, gate);
+    h->tracing = tracing;
+    return rc;
 }
+
+size_t mkv_noalloc_scratch_bytes(void) { return SCRATCH_FLOATS * sizeof(float); }
 
 int mkv_prefill(mkv_t* h, int layer, const float* q, int T, int n, int start, float scale, float* out,
                 const float* gate) {
@@ -471,6 +485,15 @@ static int snap_copy(mkv_t* h, int p, void* host, const void* chost, size_t byte
     if (bytes != mkv_snapshot_bytes(h, p))
         return fail(MKV_E_SIZE, "%s: %zu bytes given, %zu needed for %d positions", who, bytes,
                     mkv_snapshot_bytes(h, p), p);
+    {
+        // the copies are asynchronous on the stream: only pinned host memory may take them (pageable memory would
+        // make the runtime stage and block, and a restore would read the caller's buffer after this call returns)
+        hipPointerAttribute_t a{};
+        const hipError_t pe = hipPointerGetAttributes(&a, save ? host : chost);
+        if (pe != hipSuccess) (void)hipGetLastError();  // an unknown (pageable) pointer: clear the error it recorded
+        if (pe != hipSuccess || a.type != hipMemoryTypeHost)
+            return fail(MKV_E_ARG, "%s: the host buffer is not pinned host memory (hipHostMalloc)", who);
+    }
     if (p == 0) {
         if (!save) h->len.assign(h->g.layers, 0);
         return MKV_OK;

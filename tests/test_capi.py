@@ -132,3 +132,62 @@ def test_build_keeps_packed_fp32_off_for_every_source():
     for src, extra in b.EXTRA.items():
         assert src in b.SOURCES, src
         assert not any("packed-fp32" in x for x in extra), (src, extra)
+
+
+def test_build_refuses_unreviewed_extra_flags(monkeypatch):
+    """MKV_EXTRA_FLAGS reaches hipcc only in a development build (MKV_DEV_BUILD=1), and never when it names the
+    packed-FP32 feature: a shipped library cannot silently turn packed FP32 back on."""
+    from mechta_amd import build as b
+    monkeypatch.delenv("MKV_DEV_BUILD", raising=False)
+    monkeypatch.delenv("MKV_EXTRA_FLAGS", raising=False)
+    assert b._extra_flags() == []
+    monkeypatch.setenv("MKV_EXTRA_FLAGS", "-DFL_FUSE_NCH=4")
+    with pytest.raises(RuntimeError):
+        b._extra_flags()
+    monkeypatch.setenv("MKV_DEV_BUILD", "1")
+    assert b._extra_flags() == ["-DFL_FUSE_NCH=4"]
+    monkeypatch.setenv("MKV_EXTRA_FLAGS", "-Xclang -target-feature -Xclang +packed-fp32-ops")
+    with pytest.raises(RuntimeError):
+        b._extra_flags()
+    with pytest.raises(RuntimeError):  # the compile step itself refuses, before hipcc runs
+        b._compile("kv_append.hip", False)
+
+
+def test_root_path_matches_the_reference_naming(tmp_path):
+    """root-<fmt>-<model key>-<token key>.bin, the model key FNV-1a over the path's bytes each widened to a u32 token
+    (root_file / root_key, session.rs:62-73), checked against an independent FNV-1a."""
+    model = "/models/Qwen3.6-35B-A3B-UD-Q4_K_S.gguf"
+    toks = [151644, 8948, 198, 2610, 525]
+    mkey = fnv1a64(np.array(list(model.encode()), np.uint32).tobytes())
+    tkey = fnv1a64(np.array(toks, np.uint32).tobytes())
+    assert mk.root_path(str(tmp_path), mk.F16, model, toks) == f"{tmp_path}/root-f16-{mkey:016x}-{tkey:016x}.bin"
+    assert mk.root_path("/c", mk.F32, model, []).startswith(f"/c/root-f32-{mkey:016x}-{fnv1a64(b''):016x}")
+    buf = ctypes.create_string_buffer(10)
+    t = np.array(toks, np.uint32)
+    assert mk.lib().mkv_root_path(buf, 10, b"/c", mk.F16, model.encode(), t.ctypes.data_as(ctypes.c_void_p),
+                                  t.size) == mk.E_SIZE
+    assert mk.lib().mkv_root_path(buf, 10, b"/c", 7, model.encode(), None, 0) == mk.E_ARG
+    assert mk.ROOT_MIN == 2048
+
+
+def test_root_prune_keeps_the_most_recent(tmp_path):
+    """prune_roots (session.rs:75-84): only root-<fmt>-*.bin files count; the `keep` newest stay, at least one;
+    mkv_root_touch makes a file the newest."""
+    for i in range(8):
+        f = tmp_path / f"root-f16-m-{i:02d}.bin"
+        f.write_bytes(b"x")
+        os.utime(f, (1000 + i, 1000 + i))
+    for name in ("root-f32-m-00.bin", "root-f16-m-99.bin.tmp", "other.bin"):
+        (tmp_path / name).write_bytes(b"y")
+        os.utime(tmp_path / name, (1, 1))
+    mk.root_touch(str(tmp_path / "root-f16-m-00.bin"))  # oldest becomes newest
+    assert mk.root_prune(str(tmp_path), mk.F16, 6) == 2
+    left = sorted(p.name for p in tmp_path.iterdir())
+    assert left == ["other.bin", "root-f16-m-00.bin", "root-f16-m-03.bin", "root-f16-m-04.bin", "root-f16-m-05.bin",
+                    "root-f16-m-06.bin", "root-f16-m-07.bin", "root-f16-m-99.bin.tmp", "root-f32-m-00.bin"]
+    assert mk.root_prune(str(tmp_path), mk.F16, 0) == 5  # keep at least one: the newest
+    assert (tmp_path / "root-f16-m-00.bin").exists()
+    assert mk.root_prune(str(tmp_path / "missing"), mk.F16, 6) == 0
+    with pytest.raises(mk.MkvError) as e:
+        mk.root_touch(str(tmp_path / "missing.bin"))
+    assert e.value.code == mk.E_IO

@@ -350,6 +350,29 @@ def test_stale_nan_rows_past_the_length(torch_gpu, mk, fmt):
 
 # ------------------------------------------------------------------------------------------------ snapshot -------
 
+def test_snapshot_refuses_unpinned_host_memory(torch_gpu, mk):
+    """The C ABI itself refuses a pageable (or device) buffer for the asynchronous snapshot copies, with MKV_E_ARG and
+    nothing enqueued, whatever the Python wrapper checks; pinned memory of the same size is taken."""
+    import ctypes
+    torch = torch_gpu
+    print("snapshot unpinned", flush=True)
+    with mk.KvStore(2, 4096, F16) as a:
+        fill(torch, a, 0, F16, 300, seed=830)
+        fill(torch, a, 1, F16, 300, seed=831)
+        nb = a.snapshot_bytes(256)
+        L = mk.lib()
+        for buf in (torch.zeros(nb, dtype=torch.uint8), torch.zeros(nb, dtype=torch.uint8, device="cuda")):
+            for fn in (L.mkv_snapshot, L.mkv_restore):
+                rc = fn(a._h, 256, ctypes.c_void_p(buf.data_ptr()), nb)
+                assert rc == mk.E_ARG, (fn.__name__, rc)
+                assert b"pinned" in L.mkv_last_error()
+        pinned = torch.zeros(nb, dtype=torch.uint8, pin_memory=True)
+        assert L.mkv_snapshot(a._h, 256, ctypes.c_void_p(pinned.data_ptr()), nb) == 0
+        assert L.mkv_restore(a._h, 256, ctypes.c_void_p(pinned.data_ptr()), nb) == 0
+        a.sync()
+        assert a.length(0) == 256
+
+
 @pytest.mark.parametrize("fmt,p", [(F16, 1000), (F16, 1024), (F32, 777), (F16, 1)])
 def test_snapshot_roundtrip(torch_gpu, mk, fmt, p):
     torch = torch_gpu
