@@ -185,7 +185,7 @@ def bench_decode(torch, mk, steps, warmup):
     layer i % DEC_LAYERS; after the last layer of a position the length is rolled back by 2 (2 drafts rejected) and
     the next position starts 2 further, as the model's decode does."""
     N0, NT, L = 65536, 4, DEC_LAYERS
-    total = warmup + 2 * steps
+    total = warmup + 3 * steps
     ngroups = (total + L - 1) // L
     ctx = ((N0 + 2 * ngroups + NT + 1023) // 1024) * 1024
     gen = torch.Generator(device="cuda")
@@ -203,15 +203,52 @@ def bench_decode(torch, mk, steps, warmup):
     gtabs = rope_tabs(torch, mk, N0, N0 + 2 * ngroups + NT + 1)
     kend_sum = 0
 
+    # the C ABI called directly with every step's device pointers taken before timing, so the host issues a step in
+    # far less time than the GPU runs it (the Python wrapper's argument checks took about as long as a step)
+    import ctypes
+    lib, h, P = mk.lib(), st.handle, ctypes.c_void_p
+    args = [(i % L, N0 + 2 * (i // L), P(kn[i].data_ptr()), P(v[i].data_ptr()),
+             P(gtabs[2 * (i // L) + 1].data_ptr()), P(q[i].data_ptr())) for i in range(total)]
+    outp = P(out.data_ptr())
+
     def step(i):
         nonlocal kend_sum
-        layer, pos = i % L, N0 + 2 * (i // L)
-        st.append_decode(layer, pos + 1, kn[i], v[i], gtabs[pos + 1 - N0:pos + 1 - N0 + NT], q[i], out=out)
+        layer, pos, a, b, c, d = args[i]
+        rc = lib.mkv_append_decode(h, layer, pos + 1, NT, a, b, c, d, 0, 1.0 / 16, outp, None)
+        if rc != 0:
+            raise mk.MkvError(rc, lib.mkv_last_error().decode())
         kend_sum += pos + NT
         if layer == L - 1:
             st.set_len(pos + 2)  # 2 of the 3 drafts rejected: roll back before the next position's appends
 
     for i in range(warmup):
+        step(i)
+    # then about 60 ms more of the same steps (untimed): the part's clocks ramp under sustained work, and the decode
+    # kernel of the first few hundred steps measured about 1 us slower than the same launches repeated afterwards.
+    # They re-verify the position step `warmup` will take, each round of layers rolled back; the warm-up's own last,
+    # partial round of layers is then repeated, so every layer's length is what the W steps left.
+    wpos = N0 + 2 * (warmup // L)
+    wi = iter(range(10 ** 9))
+
+    def warm_step():
+        i = next(wi)
+        layer = i % L
+        st.append_decode(layer, wpos + 1, kn[i % total], v[i % total], gtabs[wpos + 1 - N0:wpos + 1 - N0 + NT],
+                         q[i % total], out=out)
+        if layer == L - 1:
+            st.set_len(wpos)
+    st.set_len(wpos)
+    warm(torch, warm_step, ms=float(os.environ.get("MKV_BENCH_WARM_MS", "60")))
+    while True:  # finish the round of layers (every length back at wpos)
+        j = next(wi)
+        if j % L == 0:
+            break
+        layer = j % L
+        st.append_decode(layer, wpos + 1, kn[j % total], v[j % total], gtabs[wpos + 1 - N0:wpos + 1 - N0 + NT],
+                         q[j % total], out=out)
+        if layer == L - 1:
+            st.set_len(wpos)
+    for i in range(warmup // L * L, warmup):
         step(i)
     torch.cuda.synchronize()
     kend_sum = 0
@@ -225,20 +262,39 @@ def bench_decode(torch, mk, steps, warmup):
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1)
     kend_mean = kend_sum / steps
-    # second pass, the next K steps, every kernel timed by its dispatch (library trace spans)
+    # then every kernel timed by its dispatch (library trace spans): the next K steps once to settle (the first few
+    # hundred traced launches of a process measured about 1 us longer per decode launch than the same launches
+    # traced again), then the K steps after them, whose spans are the figures
     st.trace(True)
     for i in range(warmup + steps, warmup + 2 * steps):
         step(i)
+    st.trace_read()
+    st.trace(False)
+    kend_sum = 0
+    st.trace(True)
+    for i in range(warmup + 2 * steps, warmup + 3 * steps):
+        step(i)
     spans = st.trace_read()
     st.trace(False)
-    kend_mean2 = (kend_sum - kend_mean * steps) / steps
+    kend_mean2 = kend_sum / steps
+    # third pass: the recorded steps again as plain decodes (their rows are written; the last position's group
+    # is left out, its 4 tokens reach past the rolled-back length), so the fused append's share of the decode kernel
+    # is the difference of the two passes' core times
+    st.trace(True)
+    for i in range(warmup + 2 * steps, warmup + 3 * steps - L):
+        layer, pos, _, _, _, d = args[i]
+        rc = lib.mkv_decode(h, layer, d, NT, pos + 1, 0, 1.0 / 16, outp, None)
+        if rc != 0:
+            raise mk.MkvError(rc, lib.mkv_last_error().decode())
+    spans_plain = st.trace_read()
+    st.trace(False)
     # CPU baseline sample: layer 0's first N0 rows plus room for the 4 appended ones
     cache_rows = (st.read_rows(0, mk.K, 0, N0), st.read_rows(0, mk.V, 0, N0))
     last = dict(q=q[total - 1].cpu().numpy(), kn=kn[0].cpu().numpy(), v=v[0].cpu().numpy(),
                 tab=gtabs[1:1 + NT].cpu().numpy(), n=N0 - NT + 1)
     st.close()
     return dict(ms=ms, wall=wall, steps=steps, kend=kend_mean, kend2=kend_mean2, spans=spans, ctx=ctx,
-                cache=cache_rows, last=last, layers=L)
+                cache=cache_rows, last=last, layers=L, spans_plain=spans_plain)
 
 
 def bench_prefill(torch, mk, steps, warmup):
@@ -278,7 +334,9 @@ def bench_prefill(torch, mk, steps, warmup):
     pairs = T * N0 + T * (T + 1) // 2
     flops = 4 * 256 * 16 * pairs
     core_ms = spans["core"][0] / max(spans["core"][1], 1)
-    return dict(ms=ms, tok_s=T / (ms * 1e-3), flops=flops, core_ms=core_ms, core_launches=spans["core"][1] / steps)
+    append_ms = spans["kv_write"][0] / max(spans["kv_write"][1], 1)
+    return dict(ms=ms, tok_s=T / (ms * 1e-3), flops=flops, core_ms=core_ms, core_launches=spans["core"][1] / steps,
+                append_ms=append_ms, T=T)
 
 
 def bench_cfg1(torch, mk, steps):
@@ -598,6 +656,36 @@ def bench_mfma_rate(wgs=512, iters=4000, reps=20):
             "what": "dense f16 MFMA chains from registers only, 2 waves per SIMD, after a 60 ms warm-up"}
 
 
+def bench_launch_floor(torch, nbytes, nbuf=10, reps=200):
+    """What two launches back to back cost at least (libmkv_probe.so), for a step of a decode launch reading nbytes
+    and a merge launch: the best back-to-back time per launch of a plain streaming read of nbytes (over a few launch
+    shapes) plus that of an empty launch of the decode's shape. Microseconds."""
+    import ctypes
+    here = os.path.dirname(os.path.abspath(__file__))
+    probe = ctypes.CDLL(os.path.join(here, "mechta_amd", "lib", "libmkv_probe.so"))
+    unit = 512 * 8 * 16  # one 64 KB stage of a 512-thread work-group
+    nbytes = (nbytes + unit - 1) // unit * unit
+    bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(nbuf)]
+    torch.cuda.synchronize()
+    ptrs = (ctypes.c_void_p * nbuf)(*[b.data_ptr() for b in bufs])
+
+    def wall(wgs, nb):
+        mean, best, w = ctypes.c_float(), ctypes.c_float(), ctypes.c_float()
+        rc = probe.mkv_probe_run(ptrs, nbuf, ctypes.c_size_t(nb), wgs, 512, 2, 1, 1, ctypes.c_size_t(0), reps,
+                                 ctypes.byref(mean), ctypes.byref(best), ctypes.byref(w))
+        if rc != 0:
+            raise RuntimeError(f"mkv_probe_run failed: HIP error {rc}")
+        return w.value
+    stages = nbytes // unit
+    read = min(wall(g, nbytes) for g in sorted({stages, max(1, stages // 2), min(248, stages * 2)}))
+    empty = wall(max(1, stages // 2), 0)
+    del bufs
+    return {"bytes": nbytes, "read_us": round(read, 2), "empty_launch_us": round(empty, 2),
+            "floor_us": round(read + empty, 2),
+            "what": "back to back: one launch of a plain streaming read of the step's K+V bytes (best of 3 shapes) "
+                    "plus one empty launch (libmkv_probe.so)"}
+
+
 def probe_sweep(torch, nbytes=134348800, nbuf=10, reps=60):
     """The plain-read probe (libmkv_probe.so) over launch shapes, for the bytes of one cfg2 decode launch, over nbuf
     buffers in turn (nothing from the last-level cache). Prints a markdown table: per shape the launch duration from
@@ -781,10 +869,23 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC["decode_f16"],
                      "kernel": "decode_f16", "bytes_per_launch": int(core_bytes)},
     }
+    plain_ms, plain_n = dec["spans_plain"]["core"]
+    core_plain_us = plain_ms / max(plain_n, 1) * 1e3
+    # the fused append at cfg2: 4 tokens x (K normed + V inputs in f32, RoPE rows) read, 4 rows of K and V written (f16)
+    append_bytes4 = 4 * (2 * 256 * 4 + 512 * 4 + 64 * 4) + 4 * 2 * 2 * 256 * 2
+    res["append"] = {"cfg2_fused_4_rows": {"core_with_append_us": round(core_avg_ms * 1e3, 2),
+                                           "core_plain_decode_us": round(core_plain_us, 2),
+                                           "incremental_us": round(core_avg_ms * 1e3 - core_plain_us, 2),
+                                           "bytes": append_bytes4}}
     if not args.no_prefill:
         pf = bench_prefill(torch, mk, max(10, args.steps // 5), 5)
         res["prefill_tok_s"] = round(pf["tok_s"], 1)
         res["prefill_ms"] = round(pf["ms"], 4)
+        # append_kernel of the 512-token block: f32 K normed, V and RoPE rows read, f16 K and V rows written
+        ab = pf["T"] * (2 * 256 * 4 + 512 * 4 + 64 * 4) + pf["T"] * 2 * 2 * 256 * 2
+        agbs = ab / (pf["append_ms"] * 1e-3) / 1e9
+        res["append"]["cfg3_512_tokens"] = {"us": round(pf["append_ms"] * 1e3, 2), "bytes": ab, "gbps": round(agbs, 1),
+                                            "frac": round(agbs / HBM_PEAK_GBS, 4), "kernel": "append_kernel"}
         if pf["core_launches"] == 1:
             tf = pf["flops"] / (pf["core_ms"] * 1e-3) / 1e12
             res["roofline_prefill"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_MFMA_PEAK_TFLOPS,
@@ -792,6 +893,7 @@ def main():
                                        "traffic": TRAFFIC["prefill_f16"], "kernel": "prefill_f16"}
     if not args.no_extra:
         res["cfg1_us_per_step"] = round(bench_cfg1(torch, mk, 200), 2)
+        res["cfg1_floor"] = bench_launch_floor(torch, 4097 * 2 * 256 * 2 * 2)
         us4, gbs4 = bench_cfg4(torch, mk, 20)
         res["cfg4_us_per_position_10_layers"] = round(us4, 1)
         res["cfg4_kv_read_gbps"] = round(gbs4, 1)

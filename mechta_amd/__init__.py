@@ -235,6 +235,12 @@ class KvStore:
     def __exit__(self, *a):
         self.close()
 
+    @property
+    def handle(self):
+        """The store's mkv_t* (ctypes.c_void_p), for a caller that calls the C ABI through lib() directly (bench.py's
+        step loops: no Python argument checks between launches)."""
+        return self._h
+
     def set_stream(self, stream):
         self._stream = stream
         _check(lib().mkv_set_stream(self._h, ctypes.c_void_p(stream.cuda_stream)))

@@ -224,10 +224,10 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
             const half8 q0 = *(const half8*)&qs[l16][128 * dh + 32 * s + 8 * g4];
             const half8 q1 = *(const half8*)&qs[16 + l16][128 * dh + 32 * s + 8 * g4];
             s4[0] = mfma16(kk[s], q0, s4[0]);
-            s4[1] = mfma16(kk[s], q1, s4[1]);
+            if (ntb > 2) s4[1] = mfma16(kk[s], q1, s4[1]);
             if constexpr (EXACT) {
                 s4[0] = mfma16(kk[s], *(const half8*)&qsl[l16][128 * dh + 32 * s + 8 * g4], s4[0]);
-                s4[1] = mfma16(kk[s], *(const half8*)&qsl[16 + l16][128 * dh + 32 * s + 8 * g4], s4[1]);
+                if (ntb > 2) s4[1] = mfma16(kk[s], *(const half8*)&qsl[16 + l16][128 * dh + 32 * s + 8 * g4], s4[1]);
             }
         }
         return [&, s4, buf]() {
@@ -406,6 +406,8 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
     const int t = blockIdx.x / QH, head = blockIdx.x % QH, dq = blockIdx.y, tid = threadIdx.x;
     const int kvh = head / GQA, row = t * GQA + head % GQA;
     const float* p = part + ((size_t)kvh * rpk + row) * nch * PART;
+    // the gate logit of this thread's output dim, loaded with the partials (one round trip for both)
+    const float gl = gate && tid < 64 ? gate[((size_t)t * QH + head) * 512 + 256 + dq * 64 + tid] : 0.f;
     int c0, c1;  // chunks holding a key of [start, n + t)
     chunk_range(start, n + t, span, nch, c0, c1);
     __shared__ float red[4];
@@ -461,10 +463,7 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
         }
         const int d = dq * 64 + tid;
         float o = sum / lt;
-        if (gate) {
-            const float g = gate[((size_t)t * QH + head) * 512 + 256 + d];
-            o = o * (1.f / (1.f + expf(-g)));
-        }
+        if (gate) o = o * (1.f / (1.f + expf(-gl)));
         const size_t oi = ((size_t)t * QH + head) * HD + d;
         if constexpr (H16) ((unsigned short*)out)[oi] = f2h(o);
         else ((float*)out)[oi] = o;
@@ -484,6 +483,9 @@ __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part,
     const float* p = part + ((size_t)kvh * rpk + row) * nch * PART;
     int c0, c1;  // chunks holding a key of [start, n + t)
     chunk_range(start, n + t, span, nch, c0, c1);
+    // the gate logits of this thread's 4 output dims, loaded with the partials (one round trip for both)
+    const float4 gl = gate ? *(const float4*)(gate + ((size_t)t * QH + head) * 512 + 256 + d0)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
     // the row's chunks in groups of MERGE_FEW, each group loaded in one round trip and folded into a running
     // (maximum, sum, accumulator); with one group this is the plain max-then-sum of the partials
     float M = NEG_INF, L = 0.f;
@@ -526,11 +528,10 @@ __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part,
     }
     float4 o = make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
     if (gate) {
-        const float4 g = *(const float4*)(gate + ((size_t)t * QH + head) * 512 + 256 + d0);
-        o.x *= 1.f / (1.f + expf(-g.x));
-        o.y *= 1.f / (1.f + expf(-g.y));
-        o.z *= 1.f / (1.f + expf(-g.z));
-        o.w *= 1.f / (1.f + expf(-g.w));
+        o.x *= 1.f / (1.f + expf(-gl.x));
+        o.y *= 1.f / (1.f + expf(-gl.y));
+        o.z *= 1.f / (1.f + expf(-gl.z));
+        o.w *= 1.f / (1.f + expf(-gl.w));
     }
     const size_t oi = ((size_t)t * QH + head) * HD + d0;
     if constexpr (H16) {

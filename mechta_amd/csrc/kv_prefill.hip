@@ -85,6 +85,25 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
     // the wave's part of a tile: a per-lane offset fixed for the kernel; the tile's base and LDS slot are wave-uniform
     const unsigned voff = w * PART_BYTES + lane * 16;
     const unsigned wlds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds_void*)ring + w * PART_BYTES);
+    // V rows past the written length may hold anything: each wave zeroes them in the part of tile j it copied itself,
+    // after its own copies have landed and before the barrier that hands the tile to every wave (no barrier of its own)
+    auto zero_own_tail = [&](int j) {
+        const int k0 = cs + 32 * SUB * j;
+        if (k0 + 32 * SUB <= kend) return;
+        unsigned char* Vw = ring + (j % NSLOT) * SLOT_BYTES + SUB * TILE_BYTES;
+#pragma unroll
+        for (int i = 0; i < PART_BYTES / 1024; i++) {
+            const unsigned off = voff + i * 1024;  // 8 consecutive positions of one dim: group off / 4096
+            const int key = k0 + (int)(off / 4096) * 8;
+            if (key + 8 > kend) {
+                half8 x = *(const half8*)(Vw + off);
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (key + e >= kend) x[e] = (_Float16)0.f;
+                *(half8*)(Vw + off) = x;
+            }
+        }
+    };
     auto issue = [&](int j) {  // each wave copies 1/NW of tile j's K blocks and V groups into slot j % NSLOT
         const int k0 = cs + 32 * SUB * j;
         const unsigned char* ks = (const unsigned char*)(K + (size_t)(k0 / KBLK) * (KBLK * HD));
@@ -133,22 +152,13 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
         for (int nb = 0; nb < 8; nb++) O[b][nb] = f32x16{};
     }
 
-    // V rows of the tile past the written length may hold anything: zero them in LDS so that 0 * V stays finite
-    auto zero_tail = [&](int j) {
-        unsigned short* Vz = (unsigned short*)(ring + (j % NSLOT) * SLOT_BYTES + SUB * TILE_BYTES);
-        const int k0 = cs + 32 * SUB * j;
-        for (int i = tid; i < 32 * SUB * HD; i += NW * 64)
-            if (k0 + (i >> 11) * 8 + (i & 7) >= kend) Vz[i] = 0;  // group i / 2048, position i % 8 in the group
-    };
     // S of tile j, the mask where it crosses a row's window, the online softmax (lazy reference max, O rescaled when a
     // finite reference moved) and P into pa
-    auto s_soft = [&](int j, half8(&pa)[RB][2]) {
-        const int k0 = cs + 32 * j;
+    auto s_mfma = [&](int j, f32x16(&Scur)[RB]) {
         const unsigned char* Ks = ring + (j % NSLOT) * SLOT_BYTES;
-        f32x16 Scur[RB];
 #pragma unroll
         for (int b = 0; b < RB; b++) Scur[b] = f32x16{};
-        constexpr int KP = 3;  // K operands in flight ahead of the S chain (LDS latency; registers allow 3)
+        constexpr int KP = 3;  // K operands in flight ahead of the S chain (LDS latency; 4 to 6 measured no faster)
         half8 kbuf[KP];
 #pragma unroll
         for (int s = 0; s < KP; s++) kbuf[s] = *(const half8*)(Ks + kaddr + s * 1024);
@@ -167,6 +177,9 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, KP, 0);
+    };
+    auto softmax = [&](int j, f32x16(&Scur)[RB], half8(&pa)[RB][2]) {
+        const int k0 = cs + 32 * j;
 #pragma unroll
         for (int b = 0; b < RB; b++) {
             // the causal / start mask only where this tile crosses a row's window (raw scores; the scale, log2
@@ -245,14 +258,13 @@ __global__ void __launch_bounds__(NW * 64) prefill_f16(const _Float16* __restric
     };
     for (int j = 0; j < ntiles; j++) {
         wait_tiles(min(ntiles - 1 - j, NSLOT - 2));
+        zero_own_tail(j);
         lds_barrier();  // tile j is in LDS for every wave; every wave is done with tile j - 1
         if (j + NSLOT - 1 < ntiles) issue(j + NSLOT - 1);  // into the slot of tile j - 1
-        if (cs + 32 * (j + 1) > kend) {
-            zero_tail(j);
-            lds_barrier();
-        }
+        f32x16 S[RB];
         half8 pa[RB][2];
-        s_soft(j, pa);
+        s_mfma(j, S);
+        softmax(j, S, pa);
         pv_tile(j, pa);
     }
 
