@@ -27,9 +27,15 @@ namespace {
 
 constexpr int KPS = KPS_F16;                   // keys per stage of the decode ring
 #ifndef MKV_DEC_WG
-#define MKV_DEC_WG 124
+#define MKV_DEC_WG 108
 #endif
-constexpr int DEC_WG = MKV_DEC_WG;             // most work-groups per kv head (2 x 124 on the 256 CUs)
+// most work-groups per kv head in a decode: 2 x 108 of the 256 CUs. Measured per 4-token step (fused append, decode,
+// merge; 10 layers rotated) against 124, the earlier choice, at 8,192 / 32,768 / 65,536 / 131,072 / 200,000
+// positions: 14.3 / 21.2 / 29.3 / 47.5 / 66.9 us against 14.9 / 21.5 / 29.7 / 49.7 / 69.6 us. The rate is not
+// monotone in the count: 100, 112 and 120 measured 0.3-0.9 us slower than 124 at 65,536 positions, 104 and 116 about
+// as fast as 108 there.
+constexpr int DEC_WG = MKV_DEC_WG;
+constexpr int SMALL_WG = 124;                  // small prefill blocks: most work-groups per kv head and block column
 constexpr int PS_STRIDE = KPS + 8;             // halves per P row in LDS (conflict-free 16-byte reads)
 constexpr int QS_STRIDE = HD + 8;              // halves per Q row in LDS
 constexpr int NEWMAX = 4;                      // appended rows per call
@@ -572,11 +578,13 @@ hipError_t launch_decode_core(const Geom& g, void* base, int layer, const float*
 }
 
 SmallPlan small_prefill_plan(int T, int n, int start) {
-    // the decode's stages over the whole block's keys; at most DEC_WG work-groups per (kv head, 4-token block) and
-    // about DEC_WG in all per kv head once there are several blocks (each block streams every stage)
+    // the decode's stages over the whole block's keys; at most SMALL_WG work-groups per (kv head, 4-token block) and
+    // about SMALL_WG in all per kv head once there are several blocks (each block streams every stage)
     const int nzb = (T + 3) / 4;
     DecodePlan d = decode_plan(n, T, start);
-    const int cap = max(8, DEC_WG / nzb);  // twice or four times as many splits measured slower
+    const int kend = n + T - 1, nu = (kend - d.s0 + KPS_F16 - 1) / KPS_F16;
+    d.nch = min(max(nu, 1), SMALL_WG);
+    const int cap = max(8, SMALL_WG / nzb);  // twice or four times as many splits measured slower
     d.nch = min(d.nch, cap);
     return SmallPlan{d, nzb};
 }

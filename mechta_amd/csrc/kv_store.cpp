@@ -166,7 +166,7 @@ StoreBytes store_bytes(int layers, int ctx, int fmt) {
     StoreBytes b;
     b.planes = (size_t)layers * 2 * KVH * (size_t)ctx * HD * (fmt == MKV_F16 ? 2 : 4);
     b.slack = STORE_SLACK;
-    // decode splits: f16 one per 64-position stage, at most 124; f32 at most 248
+    // decode splits: f16 one per 64-position stage, at most 108 (small prefill blocks 124); f32 at most 248
     b.max_chunks = std::min(ctx / 64 + 2, 256);
     b.decode_ws = (size_t)KVH * ROWS * b.max_chunks * PART * sizeof(float);
     b.prefill_ws = prefill_ws_max_floats() * sizeof(float);

@@ -154,9 +154,9 @@ DECODE_CASES = [  # (ctx, n0 positions already in the cache, ntok, start)
     (4096, 1, 1, 0), (4096, 31, 4, 0), (4096, 300, 4, 0), (4096, 1000, 1, 0), (4096, 4092, 4, 0),
     (8192, 4096, 1, 0), (8192, 5000, 4, 0), (8192, 2047, 2, 0), (8192, 3000, 3, 1), (8192, 3000, 4, 700),
     (20480, 20000, 4, 0), (20480, 17000, 1, 0),
-    # 64-key stages dealt to 124 work-groups per kv head: 1092 stages leave a partial round of 100 > 124 / 2 (whole
-    # stages), 1026 a round of 34 (split into half stages)
-    (70656, 69885, 4, 0), (66560, 65660, 4, 0), (66560, 65600, 1, 3000),
+    # 64-key stages dealt to 108 work-groups per kv head: 1150 stages leave a partial round of 70 > 108 / 2 (whole
+    # stages), 1092 a round of 12 and 1026 a round of 54 = 108 / 2 (split into half stages)
+    (74752, 73590, 4, 0), (70656, 69885, 4, 0), (66560, 65660, 4, 0), (66560, 65600, 1, 3000),
 ]
 
 
@@ -178,8 +178,8 @@ def test_decode_f16(torch_gpu, mk, ctx, n0, ntok, start):
 
 
 def test_decode_split_count_sequence(torch_gpu, mk):
-    """A sequence of decodes on one store whose split counts repeat and alternate (124, 79, 124, 79 with one token,
-    47, 124, 79, 124 with one token, 124): every output against the oracle (the workspace is shared by all of them)."""
+    """A sequence of decodes on one store whose split counts repeat and alternate (108, 79, 108, 79 with one token,
+    47, 108, 79, 108 with one token, 108): every output against the oracle (the workspace is shared by all of them)."""
     torch = torch_gpu
     with mk.KvStore(1, 12288, F16) as st:
         fill(torch, st, 0, F16, 10000, seed=77)
