@@ -293,9 +293,9 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
 Attn32Plan attn32_plan(int T, int n, int start) {
     // the window's tiles dealt round robin, four per work-group, to at most 248 work-groups per kv head (registers
     // held to 256 per lane, so two work-groups share a CU past 256 of them): at 16,384 positions (128 per kv head) the
-    // core takes 21.3-21.5 us, with two tiles per work-group (248) 24.7 us; per cfg5 verify (16,384 positions) three or
-    // five tiles per work-group measured 30.0 and 27.0 us against 24.5, at most 108 work-groups 24.9 us. Every work-group holds keys of every row,
-    // so the merge reads all (span 0)
+    // core takes 21.3-21.5 us, with two tiles per work-group (248) 24.7 us; per cfg5 verify three or five tiles per
+    // work-group measured 30.0 and 27.0 us against 24.5, at most 108 work-groups 24.9 us. Every work-group holds keys
+    // of every row, so the merge reads all (span 0)
     const int kend = n + T - 1;
     int nch = (kend - start / TILE * TILE) / 128;
     nch = nch > 248 ? 248 : nch < 1 ? 1 : nch;
