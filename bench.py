@@ -69,7 +69,7 @@ def parse():
 # HBM bytes per launch of the two kernels at the bench's workloads, from the FETCH_SIZE and WRITE_SIZE counters
 # (rocprofv3 --pmc of "bench.py --steps 20 --warmup 2 --no-cpu --no-extra --calib-copy", summarized by --pmc-summary; the
 # counters are scaled by what they read for the 256 MiB copy of --calib-copy: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0).
-TRAFFIC = {"decode_f16": 143.59e6, "prefill_f16": 163.29e6}
+TRAFFIC = {"decode_f16": 142.52e6, "prefill_f16": 163.27e6}
 
 
 def counter_summary(d):

@@ -9,7 +9,7 @@
  * (wgsl/ops.wgsl:165, wgsl/kv.wgsl:7-8); f16 caches are arrays of IEEE binary16 bit patterns (uint16_t), two per
  * u32 word in the reference's packing (pack2x16float: low half = even element), which is the same byte order.
  *
- * Fixed conventions where WGSL leaves the result open (both stated by the task's north star / survey):
+ * Fixed conventions where WGSL leaves the result open (both fixed by the task statement):
  *   - pack2x16float and f16(x) round to nearest even (orc_f32_to_f16);
  *   - a*b - c*d in kv_src is NOT fused: each product is rounded to f32, then the sum (build with -ffp-contract=off).
  *
