@@ -65,3 +65,49 @@ def test_noalloc_verify_equals_the_workspace_entry(torch_gpu, fmt):
                 ref = O.gate(att, g.cpu().numpy()).reshape(ntok, 16, 256)
                 tol = {} if fmt == F16 else {"atol": 1e-5, "rtol": 1e-5}
                 assert_attn_close(ob.cpu().numpy(), ref, what="noalloc vs oracle", **tol)
+
+
+def test_noalloc_records_no_trace_and_replays_under_capture(torch_gpu):
+    """The no-allocation call takes no trace events, even with the handle's trace on (taking them may create events
+    and grows a host list), and it captures into a HIP graph (global capture mode, where an allocation would fail the
+    capture) whose replays, with eager work of the same store in between, equal the eager call bit for bit."""
+    import mechta_amd as mk
+    torch = torch_gpu
+    lib = mk.lib()
+    n0, ntok = 3000, 4
+    print("noalloc: trace and capture", flush=True)
+    kn, v = kv_inputs(181, n0 + ntok)
+    tab = O.rope_tables(0, n0 + ntok)
+    q = _dev(torch, q_inputs(182, ntok))
+    with mk.KvStore(1, 8192, F16) as st:
+        for p in range(0, n0 - 1, 512):
+            m = min(512, n0 - 1 - p)
+            st.append(0, p, _dev(torch, kn[p:p + m]), _dev(torch, v[p:p + m]), _dev(torch, tab[p:p + m]))
+        ins = [_dev(torch, x[n0 - 1:n0 - 1 + ntok]) for x in (kn, v, tab)]
+        st.trace(True)
+        out_e = torch.full((ntok, 16, 256), float("nan"), device="cuda")
+        rc = lib.mkv_append_decode_noalloc(st.handle, 0, n0, ntok, *[_p(x) for x in ins], _p(q), 0, 1.0 / 16,
+                                           _p(out_e), None)
+        assert rc == 0, lib.mkv_last_error()
+        spans = st.trace_read()
+        assert spans["core"][1] == 0 and spans["merge"][1] == 0, spans
+        assert torch.isfinite(out_e).all()
+        st.set_len(n0 - 1)
+        out_g = torch.empty((ntok, 16, 256), device="cuda")
+        g = torch.cuda.CUDAGraph()
+        base = torch.cuda.current_stream()
+        with torch.cuda.graph(g):
+            st.set_stream(torch.cuda.current_stream())
+            rc = lib.mkv_append_decode_noalloc(st.handle, 0, n0, ntok, *[_p(x) for x in ins], _p(q), 0, 1.0 / 16,
+                                               _p(out_g), None)
+        st.set_stream(base)
+        assert rc == 0, lib.mkv_last_error()
+        st.trace(False)
+        for r in range(3):
+            out_g.fill_(float("nan"))
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out_g, out_e), f"replay {r} differs from the eager call"
+            other = st.decode(0, q, n0 - 700)
+            torch.cuda.synchronize()
+            assert torch.isfinite(other).all()
