@@ -335,8 +335,9 @@ def bench_prefill(torch, mk, steps, warmup):
     flops = 4 * 256 * 16 * pairs
     core_ms = spans["core"][0] / max(spans["core"][1], 1)
     append_ms = spans["kv_write"][0] / max(spans["kv_write"][1], 1)
+    merge_ms = spans["merge"][0] / max(spans["merge"][1], 1)
     return dict(ms=ms, tok_s=T / (ms * 1e-3), flops=flops, core_ms=core_ms, core_launches=spans["core"][1] / steps,
-                append_ms=append_ms, T=T)
+                append_ms=append_ms, merge_ms=merge_ms, T=T)
 
 
 def bench_cfg1(torch, mk, steps):
