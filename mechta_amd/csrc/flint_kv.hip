@@ -980,17 +980,18 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
 // splits of a row loaded in one round trip.
 constexpr int MERGE_FEW = 16;
 
+template <int NJ>  // at most NJ splits
 __global__ void __launch_bounds__(256) fl_merge_few(const float* __restrict__ part, int T, int nch,
                                                     const float* __restrict__ sinks, float* __restrict__ out) {
     const int rowid = blockIdx.x * 8 + (threadIdx.x >> 5);  // t * 32 + head
     if (rowid >= T * QH) return;
     const int t = rowid / QH, head = rowid % QH, d0 = (threadIdx.x & 31) * 4;
     const float* p = part + ((size_t)(head / GQA) * T * GQA + (size_t)t * GQA + head % GQA) * nch * PART;
-    float mj[MERGE_FEW], lj[MERGE_FEW];
-    f32x4 aj[MERGE_FEW];
+    float mj[NJ], lj[NJ];
+    f32x4 aj[NJ];
     float M = sinks ? sinks[head] * LOG2E : NEG_INF;
 #pragma unroll
-    for (int j = 0; j < MERGE_FEW; j++) {
+    for (int j = 0; j < NJ; j++) {
         mj[j] = NEG_INF;
         lj[j] = 0.f;
         aj[j] = f32x4{};
@@ -1005,7 +1006,7 @@ __global__ void __launch_bounds__(256) fl_merge_few(const float* __restrict__ pa
     float L = sinks && M != NEG_INF ? exp2f(sinks[head] * LOG2E - M) : 0.f;
     f32x4 acc = f32x4{};
 #pragma unroll
-    for (int j = 0; j < MERGE_FEW; j++) {
+    for (int j = 0; j < NJ; j++) {
         const float e = mj[j] == NEG_INF ? 0.f : exp2f(mj[j] - M);
         L += e * lj[j];
         acc += e * aj[j];
@@ -1074,8 +1075,12 @@ hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const 
     }
     if (e != hipSuccess) return e;
     if (p.nch > 8 * MERGE_J) return hipErrorInvalidValue;
+    // the smallest unrolled build that holds the plan's splits (each chunk slot is a predicated load)
+    const dim3 g8((T * QH + 7) / 8);
+    if (p.nch <= 4) return launch(fl_merge_few<4>, g8, dim3(256), L, (const float*)ws, T, p.nch, sinks, out);
+    if (p.nch <= 8) return launch(fl_merge_few<8>, g8, dim3(256), L, (const float*)ws, T, p.nch, sinks, out);
     if (p.nch <= MERGE_FEW)
-        return launch(fl_merge_few, dim3((T * QH + 7) / 8), dim3(256), L, (const float*)ws, T, p.nch, sinks, out);
+        return launch(fl_merge_few<MERGE_FEW>, g8, dim3(256), L, (const float*)ws, T, p.nch, sinks, out);
     return launch(fl_merge, dim3(T * QH), dim3(256), L, (const float*)ws, T, p.nch, sinks, out);
 }
 
