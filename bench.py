@@ -229,25 +229,24 @@ def bench_decode(torch, mk, steps, warmup):
     # partial round of layers is then repeated, so every layer's length is what the W steps left.
     wpos = N0 + 2 * (warmup // L)
     wi = iter(range(10 ** 9))
+    wtab = P(gtabs[wpos + 1 - N0].data_ptr())
 
-    def warm_step():
-        i = next(wi)
+    def warm_one(i):
         layer = i % L
-        st.append_decode(layer, wpos + 1, kn[i % total], v[i % total], gtabs[wpos + 1 - N0:wpos + 1 - N0 + NT],
-                         q[i % total], out=out)
+        _, _, a, b, _, d = args[i % total]
+        rc = lib.mkv_append_decode(h, layer, wpos + 1, NT, a, b, wtab, d, 0, 1.0 / 16, outp, None)
+        if rc != 0:
+            raise mk.MkvError(rc, lib.mkv_last_error().decode())
         if layer == L - 1:
             st.set_len(wpos)
+
     st.set_len(wpos)
-    warm(torch, warm_step, ms=float(os.environ.get("MKV_BENCH_WARM_MS", "60")))
+    warm(torch, lambda: warm_one(next(wi)), ms=60.0)
     while True:  # finish the round of layers (every length back at wpos)
         j = next(wi)
         if j % L == 0:
             break
-        layer = j % L
-        st.append_decode(layer, wpos + 1, kn[j % total], v[j % total], gtabs[wpos + 1 - N0:wpos + 1 - N0 + NT],
-                         q[j % total], out=out)
-        if layer == L - 1:
-            st.set_len(wpos)
+        warm_one(j)
     for i in range(warmup // L * L, warmup):
         step(i)
     torch.cuda.synchronize()
