@@ -572,9 +572,8 @@ int mkv_trace(mkv_t* h, int enable) {
             h->ms[i] = 0;
             h->count[i] = 0;
         }
-        // events for the traced launches, created and recorded once here rather than while the launches are being
-        // enqueued: taken on demand, a run's first 200 cfg2 steps timed about 1 us per decode launch slower than the
-        // same steps traced again with pooled events
+        // events for the traced launches, created (and recorded once) here, so that no event is created while the
+        // traced launches are being enqueued
         while (h->pool.size() < TRACE_RESERVE) {
             hipEvent_t ev = nullptr;
             e = hipEventCreate(&ev);
