@@ -276,24 +276,34 @@ def bench_decode(torch, mk, steps, warmup):
     spans = st.trace_read()
     st.trace(False)
     kend_mean2 = kend_sum / steps
-    # third pass: the recorded steps again as plain decodes (their rows are written; the last position's group
-    # is left out, its 4 tokens reach past the rolled-back length), so the fused append's share of the decode kernel
-    # is the difference of the two passes' core times
-    st.trace(True)
-    for i in range(warmup + 2 * steps, warmup + 3 * steps - L):
-        layer, pos, _, _, _, d = args[i]
-        rc = lib.mkv_decode(h, layer, d, NT, pos + 1, 0, 1.0 / 16, outp, None)
-        if rc != 0:
-            raise mk.MkvError(rc, lib.mkv_last_error().decode())
-    spans_plain = st.trace_read()
-    st.trace(False)
+    # the fused append's share of the decode launch: rounds of the same 4-token verify of every layer at one position,
+    # with the append (A) and as a plain decode of the rows A wrote (B), alternating; the first two rounds of each
+    # settle the trace, the next AB_ROUNDS are summed
+    AB_ROUNDS = 10
+    ab = {"A": [0.0, 0], "B": [0.0, 0]}
+    for r in range(AB_ROUNDS + 2):
+        for leg in ("A", "B"):
+            st.trace(True)
+            for layer in range(L):
+                _, _, a, b, _, d = args[layer]
+                if leg == "A":
+                    rc = lib.mkv_append_decode(h, layer, wpos + 1, NT, a, b, wtab, d, 0, 1.0 / 16, outp, None)
+                else:
+                    rc = lib.mkv_decode(h, layer, d, NT, wpos + 1, 0, 1.0 / 16, outp, None)
+                if rc != 0:
+                    raise mk.MkvError(rc, lib.mkv_last_error().decode())
+            sp = st.trace_read()["core"]
+            st.trace(False)
+            if r >= 2:
+                ab[leg][0] += sp[0]
+                ab[leg][1] += sp[1]
     # CPU baseline sample: layer 0's first N0 rows plus room for the 4 appended ones
     cache_rows = (st.read_rows(0, mk.K, 0, N0), st.read_rows(0, mk.V, 0, N0))
     last = dict(q=q[total - 1].cpu().numpy(), kn=kn[0].cpu().numpy(), v=v[0].cpu().numpy(),
                 tab=gtabs[1:1 + NT].cpu().numpy(), n=N0 - NT + 1)
     st.close()
     return dict(ms=ms, wall=wall, steps=steps, kend=kend_mean, kend2=kend_mean2, spans=spans, ctx=ctx,
-                cache=cache_rows, last=last, layers=L, spans_plain=spans_plain)
+                cache=cache_rows, last=last, layers=L, ab=ab)
 
 
 def bench_prefill(torch, mk, steps, warmup):
@@ -876,13 +886,14 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC["decode_f16"],
                      "kernel": "decode_f16", "bytes_per_launch": int(core_bytes)},
     }
-    plain_ms, plain_n = dec["spans_plain"]["core"]
-    core_plain_us = plain_ms / max(plain_n, 1) * 1e3
+    (a_ms, a_n), (b_ms, b_n) = dec["ab"]["A"], dec["ab"]["B"]
+    core_ab_us, core_plain_us = a_ms / max(a_n, 1) * 1e3, b_ms / max(b_n, 1) * 1e3
     # the fused append at cfg2: 4 tokens x (K normed + V inputs in f32, RoPE rows) read, 4 rows of K and V written (f16)
     append_bytes4 = 4 * (2 * 256 * 4 + 512 * 4 + 64 * 4) + 4 * 2 * 2 * 256 * 2
-    res["append"] = {"cfg2_fused_4_rows": {"core_with_append_us": round(core_avg_ms * 1e3, 2),
+    res["append"] = {"cfg2_fused_4_rows": {"core_with_append_us": round(core_ab_us, 2),
                                            "core_plain_decode_us": round(core_plain_us, 2),
-                                           "incremental_us": round(core_avg_ms * 1e3 - core_plain_us, 2),
+                                           "incremental_us": round(core_ab_us - core_plain_us, 2),
+                                           "launches": a_n,
                                            "bytes": append_bytes4}}
     if not args.no_prefill:
         pf = bench_prefill(torch, mk, max(10, args.steps // 5), 5)
