@@ -874,7 +874,7 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
 
     // the four waves' states into one partial
     __shared__ f32x4 ob[4][8][64];
-    __shared__ float ml[4][2][16];
+    __shared__ __attribute__((aligned(16))) float ml[4][2][16];
 #pragma unroll
     for (int cc = 0; cc < 8; cc++) ob[w][cc][lane] = O[cc];
     if (g == 0) {
@@ -885,61 +885,73 @@ __global__ void __launch_bounds__(256) fl_dec16(const void* __restrict__ kplane,
     // With the merge fused (arrivals != NULL, few splits), the partial is stored device-coherent (scope bit sc1,
     // through the XCD's L2) and the kv head's last work-group to arrive merges them all; no work-group waits.
     const bool fused = arrivals != nullptr;
-    __shared__ int last;
-    if (w == 0) {
-        const size_t rbase = (size_t)kvh * T * GQA;
+    auto put = [&](float* p, float x) {
+        if (fused) __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else *p = x;
+    };
+    const size_t rbase = (size_t)kvh * T * GQA;
+    {
+        // every wave combines dims 16cc .. 16cc + 15 of cc = 2w, 2w + 1 for its lane's rows 4g + r: the rows' factors
+        // and the eight states read from LDS in one round, then the stores (no chain of dependent LDS reads)
+        f32x4 mw[4], f[4], x[2][4];
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) mw[ww] = *(const f32x4*)&ml[ww][0][4 * g];
+#pragma unroll
+        for (int c2 = 0; c2 < 2; c2++)
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) x[c2][ww] = ob[ww][2 * w + c2][lane];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float M = NEG_INF;
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) M = fmaxf(M, mw[ww][r]);
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) f[ww][r] = mw[ww][r] == NEG_INF ? 0.f : exp2f(mw[ww][r] - M);
+        }
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int row = 4 * g + r;
-            float M = NEG_INF;
-#pragma unroll
-            for (int ww = 0; ww < 4; ww++) M = fmaxf(M, ml[ww][0][row]);
-            float f[4];
-#pragma unroll
-            for (int ww = 0; ww < 4; ww++) f[ww] = ml[ww][0][row] == NEG_INF ? 0.f : exp2f(ml[ww][0][row] - M);
             if (row < T * GQA) {
                 float* p = part + ((rbase + row) * nch + c) * PART + PACC + r16;
 #pragma unroll
-                for (int cc = 0; cc < 8; cc++) {
+                for (int c2 = 0; c2 < 2; c2++) {
                     float o = 0.f;
 #pragma unroll
-                    for (int ww = 0; ww < 4; ww++) o += f[ww] * ob[ww][cc][lane][r];
-                    if (fused) __hip_atomic_store(p + 16 * cc, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    else p[16 * cc] = o;
+                    for (int ww = 0; ww < 4; ww++) o += f[ww][r] * x[c2][ww][r];
+                    put(p + 16 * (2 * w + c2), o);
                 }
             }
         }
-        if (g == 0 && r16 < T * GQA) {
-            float M = NEG_INF, Lt = 0.f;
+    }
+    if (w == 0 && g == 0 && r16 < T * GQA) {
+        float M = NEG_INF, Lt = 0.f;
 #pragma unroll
-            for (int ww = 0; ww < 4; ww++) M = fmaxf(M, ml[ww][0][r16]);
+        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, ml[ww][0][r16]);
 #pragma unroll
-            for (int ww = 0; ww < 4; ww++)
-                Lt += ml[ww][0][r16] == NEG_INF ? 0.f : exp2f(ml[ww][0][r16] - M) * ml[ww][1][r16];
-            float* p = part + ((rbase + r16) * nch + c) * PART;
-            if (fused) {
-                __hip_atomic_store(p, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(p + 1, Lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-                p[0] = M;
-                p[1] = Lt;
-            }
-        }
-        if (fused) {
-            // release at agent scope (this wave stored the whole partial): the partial happens before the arrival
-            // that counts it; the kv head's last arrival then acquires, so its merge reads every partial
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-            int l = 0;
-            if (lane == 0) {
-                l = __hip_atomic_fetch_add(arrivals + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (unsigned)(nch - 1);
-                if (l) __hip_atomic_store(arrivals + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                last = l;
-            }
-            if (__builtin_amdgcn_readfirstlane(l)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        }
+        for (int ww = 0; ww < 4; ww++)
+            Lt += ml[ww][0][r16] == NEG_INF ? 0.f : exp2f(ml[ww][0][r16] - M) * ml[ww][1][r16];
+        float* p = part + ((rbase + r16) * nch + c) * PART;
+        put(p, M);
+        put(p + 1, Lt);
     }
     if (!fused) return;
+    // every wave's partial stores complete before the work-group barrier; wave 0 then releases at agent scope: the
+    // partial happens before the arrival that counts it, and the kv head's last arrival acquires, so its merge reads
+    // every partial
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ int last;
+    if (w == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        int l = 0;
+        if (lane == 0) {
+            l = __hip_atomic_fetch_add(arrivals + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                (unsigned)(nch - 1);
+            if (l) __hip_atomic_store(arrivals + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = l;
+        }
+        if (__builtin_amdgcn_readfirstlane(l)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
     __syncthreads();  // the other waves see the acquiring wave's view through the work-group barrier
     if (!last) return;
     // the kv head's last work-group: the merge of fl_merge for its rows (row = token * 8 + head of the kv head, T * 8
