@@ -439,8 +439,9 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
         }
         M = fmaxf(M, mj[j]);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    // the wave's maximum: within each 16-lane row by DPP, then across rows (one LDS permute, one lane-half swap)
+    M = reduce16(M, [](float a, float b) { return fmaxf(a, b); });
+    M = max_xor32(fmaxf(M, __shfl_xor(M, 16)));
     if ((tid & 63) == 0) red[tid >> 6] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -459,12 +460,14 @@ __global__ void __launch_bounds__(256) decode_combine(const float* __restrict__ 
     if (dl == 0) redl[cl] = L;
     __syncthreads();
     if (tid < 64) {
+        // thread = (dim 4 dd + comp): its component of every chunk lane's sum at one constant stride, so the 16
+        // LDS reads are independent and issue together (a component chosen from a whole float4 read made a chain)
         const int dd = tid >> 2, comp = tid & 3;
+        const float* col = &acc4[0][dd].x + comp;
         float sum = 0.f, lt = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const float4 v = acc4[i][dd];
-            sum += comp == 0 ? v.x : comp == 1 ? v.y : comp == 2 ? v.z : v.w;
+            sum += col[i * 64];
             lt += redl[i];
         }
         const int d = dq * 64 + tid;
