@@ -212,6 +212,20 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
     float m_run = NEG_INF, l_run = 0.f;
     f32x16 O = f32x16{};
 
+    // Q's B operands in registers for the whole loop (rows 16hb + lane%16, dims 128dh + 32s + 8(lane/16) .. +7): read
+    // from LDS once here instead of in every stage, where a read behind the second row half's branch waited on the
+    // one before
+    half8 qb0[4], qb1[4], qbl0[EXACT ? 4 : 1], qbl1[EXACT ? 4 : 1];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        qb0[s] = *(const half8*)&qs[l16][128 * dh + 32 * s + 8 * g4];
+        qb1[s] = *(const half8*)&qs[16 + l16][128 * dh + 32 * s + 8 * g4];
+        if constexpr (EXACT) {
+            qbl0[s] = *(const half8*)&qsl[l16][128 * dh + 32 * s + 8 * g4];
+            qbl1[s] = *(const half8*)&qsl[16 + l16][128 * dh + 32 * s + 8 * g4];
+        }
+    }
+
     // S partial of this wave's 16 keys x 32 rows over its 128 dims, into ss[buf][dh]
     auto s_part = [&](int j, const StageRegs& R, int buf) {
         half8 kk[4] = {R.k[0], R.k[1], R.k[2], R.k[3]};
@@ -226,14 +240,11 @@ __global__ void __launch_bounds__(512) decode_f16(_Float16* __restrict__ kplane,
         f32x4 s4[2] = {f32x4{}, f32x4{}};
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            // B = Q^T: rows 16hb + lane%16, dims 128dh + 32s + 8(lane/16) .. +7
-            const half8 q0 = *(const half8*)&qs[l16][128 * dh + 32 * s + 8 * g4];
-            const half8 q1 = *(const half8*)&qs[16 + l16][128 * dh + 32 * s + 8 * g4];
-            s4[0] = mfma16(kk[s], q0, s4[0]);
-            if (ntb > 2) s4[1] = mfma16(kk[s], q1, s4[1]);
+            s4[0] = mfma16(kk[s], qb0[s], s4[0]);
+            if (ntb > 2) s4[1] = mfma16(kk[s], qb1[s], s4[1]);
             if constexpr (EXACT) {
-                s4[0] = mfma16(kk[s], *(const half8*)&qsl[l16][128 * dh + 32 * s + 8 * g4], s4[0]);
-                if (ntb > 2) s4[1] = mfma16(kk[s], *(const half8*)&qsl[16 + l16][128 * dh + 32 * s + 8 * g4], s4[1]);
+                s4[0] = mfma16(kk[s], qbl0[s], s4[0]);
+                if (ntb > 2) s4[1] = mfma16(kk[s], qbl1[s], s4[1]);
             }
         }
         return [&, s4, buf]() {
