@@ -37,14 +37,21 @@ __device__ inline f32x4 bload4f(rsrc_t r, unsigned voff, unsigned soff) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, LOAD_NT));
 }
 
+#ifndef ATTN32_NWV
+#define ATTN32_NWV 4
+#endif
+constexpr int NWV = ATTN32_NWV;   // waves per work-group, each over DPW of the 256 dims
+constexpr int DPW = HD / NWV;     // 64 (4 waves) or 32 (8 waves)
+constexpr int NC = DPW / 32;      // 32-dim blocks of P.V per wave
+constexpr int NTH = 64 * NWV;     // threads per work-group
 struct Tile {
-    f32x4 k[8];  // K: dims 64w + 16k + 8s + 4e .. +3 of key l % 32 (index 2k + e)
-    f32x4 v[8];  // V: keys 16k + 8e + 4s .. +3 of dim 64w + 32c + l % 32 (index 4k + 2c + e)
+    f32x4 k[DPW / 8];  // K: dims DPW w + 16k + 8s + 4e .. +3 of key l % 32 (index 2k + e)
+    f32x4 v[4 * NC];   // V: keys 16k + 8e + 4s .. +3 of dim DPW w + 32c + l % 32 (index 2 NC k + 2c + e)
 };
 
 // Two tiles in registers, one loading while the other computes (deeper prefetch measured slower from HBM: 3 tiles 2 us
 // and 4 tiles 5 us more per 16K-position decode)
-__global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
+__global__ void __launch_bounds__(NTH, NWV == 4 ? 2 : 1) attn_f32(const float* __restrict__ kplane, const float* __restrict__ vplane,
                                                 size_t plane_elems, const float* __restrict__ q, int T, int n,
                                                 int start, float scale2, int span, int nch, int c0, int nrb, int rpk,
                                                 float* __restrict__ part, const float* __restrict__ akn,
@@ -83,23 +90,25 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
     const unsigned rbytes = ntile > 0 ? (unsigned)((ntile - 1) * tstep + 1) * TILE_BYTES : 0u;
     const rsrc_t kr = plane_rsrc(kplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
     const rsrc_t vr = plane_rsrc(vplane + (size_t)kvh * plane_elems + (size_t)lo * HD, rbytes);
-    const unsigned kofs = ((16 * w + 2 * s) * TILE + r32) * 16;  // + (4k + e) * 512 B: dims 64w + 16k + 8s + 4e
-    const unsigned vofs = (s * HD + 64 * w + r32) * 16;            // + (4k + 2e) * 4 KB + c * 32 dims * 16 B
+    const unsigned kofs = (((DPW / 4) * w + 2 * s) * TILE + r32) * 16;  // + (4k + e) * 512 B: dims DPW w + 16k + 8s + 4e
+    const unsigned vofs = (s * HD + DPW * w + r32) * 16;  // + (4k + 2e) * 4 KB + c * 32 dims * 16 B
     auto load = [&](Tile& X, int j) {
         const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(j * tstep) * TILE_BYTES);
 #pragma unroll
-        for (int i = 0; i < 8; i++) X.k[i] = bload4f(kr, kofs + ((i >> 1) * 4 + (i & 1)) * (TILE * 16), base);
+        for (int i = 0; i < DPW / 8; i++) X.k[i] = bload4f(kr, kofs + ((i >> 1) * 4 + (i & 1)) * (TILE * 16), base);
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            X.v[i] = bload4f(vr, vofs + ((i >> 2) * 4 + 2 * (i & 1)) * (HD * 16) + ((i >> 1) & 1) * (32 * 16), base);
+        for (int i = 0; i < 4 * NC; i++)
+            X.v[i] = bload4f(vr, vofs + ((i / (2 * NC)) * 4 + 2 * (i & 1)) * (HD * 16) + ((i >> 1) % NC) * (32 * 16),
+                             base);
     };
 
     // Q's loads, then the first two tiles': loads complete in order, so the Q split below waits for Q only, and the
     // tiles fly while Q is split into LDS and the fused append's rows are computed
-    f32x4 xq[4][2];
+    constexpr int QI = ROWS * HD / 8 / NTH;  // 8-dim pieces of Q per thread
+    f32x4 xq[QI][2];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int i = tid + 256 * k, row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
+    for (int k = 0; k < QI; k++) {
+        const int i = tid + NTH * k, row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
         const float* qr = q + ((size_t)min(t, T - 1) * QH + kvh * GQA + (row & 7)) * HD + d8;
         xq[k][0] = *(const f32x4*)qr;
         xq[k][1] = *(const f32x4*)(qr + 4);
@@ -121,7 +130,7 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
                 apf = apl == 0 ? p : apf;
                 apl = p + 1;
             }
-        for (int i = tid; i < (apl - apf) * HD; i += 256) {
+        for (int i = tid; i < (apl - apf) * HD; i += NTH) {
             const int t = apf - apos + i / HD, d = i % HD;
             newk[i / HD][d] = rope_dim(akn + ((size_t)t * KVH + kvh) * HD, atab + (size_t)t * 64, d);
             newv[i / HD][d] = av[(size_t)t * (KVH * HD) + kvh * HD + d];
@@ -129,11 +138,11 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
     }
 
     __shared__ __attribute__((aligned(16))) _Float16 qh[ROWS][QPAD], ql[ROWS][QPAD];  // Q split: hi, lo
-    __shared__ f32x4 sx[2][4][4][64];  // partial S^T: [tile parity][wave][register quad][lane]
-    __shared__ __attribute__((aligned(16))) float cfw[4][ROWS];  // each wave's rescale factors
+    __shared__ f32x4 sx[2][NWV][4][64];  // partial S^T: [tile parity][wave][register quad][lane]
+    __shared__ __attribute__((aligned(16))) float cfw[NWV][ROWS];  // each wave's rescale factors
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int i = tid + 256 * k, row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
+    for (int k = 0; k < QI; k++) {
+        const int i = tid + NTH * k, row = i / (HD / 8), d8 = (i % (HD / 8)) * 8, t = t0 + (row >> 3);
         const f32x4 x0 = t < T ? xq[k][0] : f32x4{}, x1 = t < T ? xq[k][1] : f32x4{};
         half8 hi, lo;
         split8(x0, x1, hi, lo);
@@ -144,35 +153,37 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
 
     const int vis = n + t0 + (r32 >> 3);  // lane's row sees keys < vis (and of this split, < hi)
     float m_run = NEG_INF, l_run = 0.f;
-    f32x16 O[2] = {f32x16{}, f32x16{}};
+    f32x16 O[NC];
+#pragma unroll
+    for (int cc = 0; cc < NC; cc++) O[cc] = f32x16{};
     auto step = [&](Tile& X, int j) {
         const int k0 = lo + j * tstep * TILE;
         if (k0 < apl && k0 + TILE > apf) {  // the tile holds new rows: their K and V from LDS
             const int key = k0 + r32;
             if (key >= apf && key < apl) {
 #pragma unroll
-                for (int i = 0; i < 8; i++)
-                    X.k[i] = *(const f32x4*)&newk[key - apf][64 * w + 16 * (i >> 1) + 8 * s + 4 * (i & 1)];
+                for (int i = 0; i < DPW / 8; i++)
+                    X.k[i] = *(const f32x4*)&newk[key - apf][DPW * w + 16 * (i >> 1) + 8 * s + 4 * (i & 1)];
             }
 #pragma unroll
-            for (int i = 0; i < 8; i++)
+            for (int i = 0; i < 4 * NC; i++)
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
-                    const int kv = k0 + 16 * (i >> 2) + 8 * (i & 1) + 4 * s + b;
-                    if (kv >= apf && kv < apl) X.v[i][b] = newv[kv - apf][64 * w + 32 * ((i >> 1) & 1) + r32];
+                    const int kv = k0 + 16 * (i / (2 * NC)) + 8 * (i & 1) + 4 * s + b;
+                    if (kv >= apf && kv < apl) X.v[i][b] = newv[kv - apf][DPW * w + 32 * ((i >> 1) % NC) + r32];
                 }
         }
         f32x16 S = f32x16{};
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < DPW / 16; k++) {
             half8 kh, kl;
             split8(X.k[2 * k], X.k[2 * k + 1], kh, kl);
-            const half8 bh = *(const half8*)&qh[r32][64 * w + 16 * k + 8 * s];
-            const half8 bl = *(const half8*)&ql[r32][64 * w + 16 * k + 8 * s];
+            const half8 bh = *(const half8*)&qh[r32][DPW * w + 16 * k + 8 * s];
+            const half8 bl = *(const half8*)&ql[r32][DPW * w + 16 * k + 8 * s];
             S = mfma3(kh, kl, bh, bl, S);
         }
         float sv[16];
-        f32x4(&sg)[4][4][64] = sx[j & 1];
+        f32x4(&sg)[NWV][4][64] = sx[j & 1];
 #pragma unroll
         for (int a = 0; a < 4; a++) sg[w][a][lane] = f32x4{S[4 * a], S[4 * a + 1], S[4 * a + 2], S[4 * a + 3]};
         lds_barrier();  // parity buffers: a group's round i + 2 writes pb again only after every wave passed round i + 1
@@ -180,8 +191,16 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
         for (int a = 0; a < 4; a++) {
             const f32x4 p0 = sg[0][a][lane], p1 = sg[1][a][lane];
             const f32x4 p2 = sg[2][a][lane], p3 = sg[3][a][lane];
+            if constexpr (NWV == 4) {
 #pragma unroll
-            for (int b = 0; b < 4; b++) sv[4 * a + b] = (p0[b] + p1[b]) + (p2[b] + p3[b]);
+                for (int b = 0; b < 4; b++) sv[4 * a + b] = (p0[b] + p1[b]) + (p2[b] + p3[b]);
+            } else {
+                const f32x4 p4 = sg[4][a][lane], p5 = sg[5][a][lane];
+                const f32x4 p6 = sg[6][a][lane], p7 = sg[7][a][lane];
+#pragma unroll
+                for (int b = 0; b < 4; b++)
+                    sv[4 * a + b] = ((p0[b] + p1[b]) + (p2[b] + p3[b])) + ((p4[b] + p5[b]) + (p6[b] + p7[b]));
+            }
         }
         // exact-max online softmax in log2 units on the raw scores (scale2 > 0: the max of the scaled scores is the
         // scaled max, and the exponent is one FMA); masked scores are -inf. A tile that lies inside every row's window
@@ -219,20 +238,19 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
             for (int a = 0; a < 4; a++) {
                 const f32x4 f = *(const f32x4*)&cfw[w][8 * a + 4 * s];
 #pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    O[0][4 * a + b] *= f[b];
-                    O[1][4 * a + b] *= f[b];
-                }
+                for (int b = 0; b < 4; b++)
+#pragma unroll
+                    for (int cc = 0; cc < NC; cc++) O[cc][4 * a + b] *= f[b];
             }
             __builtin_amdgcn_wave_barrier();
         }
         // keys past the block's last (unwritten or stale rows) have P = 0 and must not bring NaN in through V
         if (k0 + TILE > hi) {
 #pragma unroll
-            for (int i = 0; i < 8; i++)
+            for (int i = 0; i < 4 * NC; i++)
 #pragma unroll
                 for (int b = 0; b < 4; b++)
-                    if (k0 + 16 * (i >> 2) + 8 * (i & 1) + 4 * s + b >= hi) X.v[i][b] = 0.f;
+                    if (k0 + 16 * (i / (2 * NC)) + 8 * (i & 1) + 4 * s + b >= hi) X.v[i][b] = 0.f;
         }
 #pragma unroll
         for (int k = 0; k < 2; k++) {
@@ -240,9 +258,9 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
             split8(f32x4{sv[8 * k], sv[8 * k + 1], sv[8 * k + 2], sv[8 * k + 3]},
                    f32x4{sv[8 * k + 4], sv[8 * k + 5], sv[8 * k + 6], sv[8 * k + 7]}, ph, pl);
 #pragma unroll
-            for (int cc = 0; cc < 2; cc++) {
+            for (int cc = 0; cc < NC; cc++) {
                 half8 vh, vl;
-                split8(X.v[4 * k + 2 * cc], X.v[4 * k + 2 * cc + 1], vh, vl);
+                split8(X.v[2 * NC * k + 2 * cc], X.v[2 * NC * k + 2 * cc + 1], vh, vl);
                 O[cc] = mfma3(ph, pl, vh, vl, O[cc]);
             }
         }
@@ -263,7 +281,7 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
     if (apl > apf) {
         float* Kp = (float*)kplane + (size_t)kvh * plane_elems;
         float* Vp = (float*)vplane + (size_t)kvh * plane_elems;
-        for (int i = tid; i < (apl - apf) * HD; i += 256) {
+        for (int i = tid; i < (apl - apf) * HD; i += NTH) {
             const int r = i / HD, d = i % HD;
             Kp[k_off32(apf + r, d)] = newk[r][d];
             Vp[v_off32(apf + r, d)] = newv[r][d];
@@ -276,9 +294,9 @@ __global__ void __launch_bounds__(256, 2) attn_f32(const float* __restrict__ kpl
     for (int i = 0; i < 16; i++) {
         const int row = 8 * (i >> 2) + 4 * s + (i & 3);
         if (t0 + (row >> 3) < T) {
-            float* p = part + ((rbase + row) * nch + c) * PART + PACC + 64 * w + r32;
-            p[0] = O[0][i];
-            p[32] = O[1][i];
+            float* p = part + ((rbase + row) * nch + c) * PART + PACC + DPW * w + r32;
+#pragma unroll
+            for (int cc = 0; cc < NC; cc++) p[32 * cc] = O[cc][i];
         }
     }
     if (w == 0 && s == 0 && t0 + (r32 >> 3) < T) {
@@ -312,7 +330,7 @@ hipError_t launch_attn_f32(const Geom& g, const void* base, int layer, const flo
     const float* vp = (const float*)(b + g.plane(layer, 1, 0) * g.plane_bytes());
     if (T > 4) return hipErrorInvalidValue;  // decode only: prefill_f32 serves blocks
     dim3 grid(p.nrb * (p.nch - p.c0) * KVH);
-    return launch(attn_f32, grid, dim3(256), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
+    return launch(attn_f32, grid, dim3(NTH), L, kp, vp, g.plane_elems, q, T, n, start, scale * LOG2E, p.span,
                   p.nch, p.c0, p.nrb, rpk, part, fa.kn, fa.v, fa.tab, fa.pos, fa.ntok);
 }
 
