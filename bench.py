@@ -537,7 +537,7 @@ def bench_flint(torch, mk, ctx=32768):
         i = [0]
         # the C ABI called directly: a one-token call takes less GPU time than the Python wrapper's checks
         import ctypes
-        lib, h, P = mf.lib(), st._h, ctypes.c_void_p
+        lib, h, P = mf.lib(), st.handle, ctypes.c_void_p
         pq1, pqb, psk, po1, pob = (P(x.data_ptr()) for x in (q1, qb, sinks, o1, ob))
 
         def attend(layer, pos0, ntok, pq, po):

@@ -91,6 +91,11 @@ class FlintStore:
         except Exception:
             pass
 
+    @property
+    def handle(self):
+        """The store's mfl_t* (ctypes.c_void_p), for a caller that calls the C ABI through lib() directly."""
+        return self._h
+
     def set_stream(self, stream):
         """Later calls enqueue on `stream` (a torch.cuda.Stream), e.g. torch's stream while capturing a graph."""
         _check(lib().mfl_set_stream(self._h, ctypes.c_void_p(stream.cuda_stream)))
