@@ -139,8 +139,8 @@ def pmc_summary(fetch_dir, write_dir):
             continue
         fk, wk = sum(fetch[key]) / len(fetch[key]), sum(write[key]) / len(write[key])
         rb, wb = fk * 1024 * f_scale / 1e6, wk * 1024 * w_scale / 1e6
-        short = next((x for x in ("decode_f16", "decode_f32", "decode_combine", "merge_few", "append_kernel",
-                                  "rows_kernel", "prefill_f16") if x in name), name[:40])
+        short = name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        short = short.replace("mkv::flint::", "").replace("mkv::", "")[:48]
         print(f"| {short} | {grid} | {len(fetch[key])} | {fk:.1f} | {wk:.1f} | {rb:.2f} | {wb:.2f} | {rb + wb:.2f} |")
 
 
