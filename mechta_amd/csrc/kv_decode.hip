@@ -566,13 +566,16 @@ __global__ void __launch_bounds__(256) merge_few(const float* __restrict__ part,
 
 DecodePlan decode_plan(int n, int ntok, int start) {
     // 64-position stages dealt round robin (neighbouring stages stream from different CUs at once, which keeps HBM
-    // busier than one contiguous range per work-group), at most DEC_WG work-groups per kv head; a short context gets
-    // one stage per work-group (all its loads in flight at once: 1 token at 4,097 positions 10.7 us per step against
-    // 11.0 us with at least 2 stages each)
+    // busier than one contiguous range per work-group), at most DEC_WG work-groups per kv head. Up to DEC_WG stages,
+    // nu / 2 + 1 work-groups take two stages each but one or two of them, the last of which takes the stage holding
+    // the appended rows (with one stage each, that work-group's append work came on top of a full share): 4 tokens at
+    // 2,048 / 4,096 / 5,632 / 6,850 positions 9.7 / 10.0 / 10.4 / 10.8 us per step against 9.9 / 10.7 / 11.3 / 11.9,
+    // 1 token at 4,097 (cfg1) 9.0 against 9.1 us. Under 32 stages, one stage each: too few work-groups stream
+    // otherwise (4 tokens at 1,024 / 1,536 positions, two stages each: 9.7 / 10.1 against 9.6 / 9.8 us).
     const int kend = n + ntok - 1;
     const int s0 = start / KPS_F16 * KPS_F16;
     const int nu = (kend - s0 + KPS_F16 - 1) / KPS_F16;
-    int g = nu;
+    int g = nu >= 32 && nu <= DEC_WG ? nu / 2 + 1 : nu;
     g = g < 1 ? 1 : g > DEC_WG ? DEC_WG : g;
     return DecodePlan{0, g, 0, s0, nu};
 }
