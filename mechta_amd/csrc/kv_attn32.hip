@@ -102,6 +102,46 @@ __global__ void __launch_bounds__(NTH, NWV == 4 ? 2 : 1) attn_f32(const float* _
                              base);
     };
 
+    // Fused append (decode only: mkv_append_decode on the f32 store). The new rows [apos, apos + antok) lie in the
+    // last one or two tiles; the work-group holding a tile computes its new rows (the same arithmetic as
+    // append_kernel) into LDS, patches them into that tile's K and V registers, and stores them to the planes after
+    // its loop: no load waits for the stores, and no other work-group reads those positions in this launch.
+    __shared__ __attribute__((aligned(16))) float newk[4][HD], newv[4][HD];
+    __shared__ __attribute__((aligned(16))) _Float16 qh[ROWS][QPAD], ql[ROWS][QPAD];  // Q split: hi, lo
+    __shared__ f32x4 sx[2][NWV][4][64];  // partial S^T of the loop: [tile parity][wave][register quad][lane]
+    // the append's inputs (K normed rows, V rows, table rows) before the loop, in the S^T exchange's second buffer: a
+    // buffer of their own would take the work-group's LDS past half of the CU's, and the compiler, counting on one
+    // work-group per CU, would then spend registers more freely (AGPR copies in the loop: 0.85 us per cfg5 verify)
+    float* const ain = (float*)&sx[1][0][0][0];
+    static_assert(sizeof(sx[1]) >= (8 * HD + 4 * 64) * sizeof(float), "the append's inputs fit the second buffer");
+    int apf = 0, apl = 0;  // this work-group's new rows [apf, apl)
+    if (antok > 0) {
+        const int lo0 = start / TILE * TILE;
+        for (int p = apos; p < apos + antok; p++)
+            if (((p - lo0) / TILE) % nch == c) {
+                apf = apl == 0 ? p : apf;
+                apl = p + 1;
+            }
+    }
+    const int nr = apl - apf;
+
+    if (nr > 0) {
+        // the append's inputs by direct loads into LDS, issued before Q's and the tiles': they complete in order, so
+        // the Q split's wait (below) covers them and not the tiles
+        const int ta = apf - apos;
+#pragma unroll
+        for (int k = 0; k < (2 * 4 + NWV) / NWV; k++) {  // 1 KB per direct load: K rows, V rows, then the table rows
+            const int i = w + NWV * k;
+            if (i < 2 * nr + 1) {
+                const float* src = i < nr       ? akn + ((size_t)(ta + i) * KVH + kvh) * HD
+                                   : i < 2 * nr ? av + (size_t)(ta + i - nr) * (KVH * HD) + kvh * HD
+                                                : atab + (size_t)ta * 64;
+                const float* dst = ain + (i < nr ? i : i < 2 * nr ? 4 + i - nr : 8) * HD;
+                if (i < 2 * nr || lane < 16 * nr) dma16s(src, lane * 16, (unsigned)(uintptr_t)(lds_void*)dst);
+            }
+        }
+    }
+
     // Q's loads, then the first two tiles': loads complete in order, so the Q split below waits for Q only, and the
     // tiles fly while Q is split into LDS and the fused append's rows are computed
     constexpr int QI = ROWS * HD / 8 / NTH;  // 8-dim pieces of Q per thread
@@ -113,32 +153,13 @@ __global__ void __launch_bounds__(NTH, NWV == 4 ? 2 : 1) attn_f32(const float* _
         xq[k][0] = *(const f32x4*)qr;
         xq[k][1] = *(const f32x4*)(qr + 4);
     }
+    // every Q load issued before the tiles' (a Q load the scheduler sank below them made the Q split wait for both
+    // tiles: 1.4 us more per launch)
+    __builtin_amdgcn_sched_barrier(0);
     Tile X[2];
     load(X[0], 0);
     load(X[1], 1);
 
-    // Fused append (decode only: mkv_append_decode on the f32 store). The new rows [apos, apos + antok) lie in the
-    // last one or two tiles; the work-group holding a tile computes its new rows here (the same arithmetic as
-    // append_kernel) into LDS, patches them into that tile's K and V registers, and stores them to the planes after
-    // its loop: no load waits for the stores, and no other work-group reads those positions in this launch.
-    __shared__ __attribute__((aligned(16))) float newk[4][HD], newv[4][HD];
-    int apf = 0, apl = 0;  // this work-group's new rows [apf, apl)
-    if (antok > 0) {
-        const int lo0 = start / TILE * TILE;
-        for (int p = apos; p < apos + antok; p++)
-            if (((p - lo0) / TILE) % nch == c) {
-                apf = apl == 0 ? p : apf;
-                apl = p + 1;
-            }
-        for (int i = tid; i < (apl - apf) * HD; i += NTH) {
-            const int t = apf - apos + i / HD, d = i % HD;
-            newk[i / HD][d] = rope_dim(akn + ((size_t)t * KVH + kvh) * HD, atab + (size_t)t * 64, d);
-            newv[i / HD][d] = av[(size_t)t * (KVH * HD) + kvh * HD + d];
-        }
-    }
-
-    __shared__ __attribute__((aligned(16))) _Float16 qh[ROWS][QPAD], ql[ROWS][QPAD];  // Q split: hi, lo
-    __shared__ f32x4 sx[2][NWV][4][64];  // partial S^T: [tile parity][wave][register quad][lane]
     __shared__ __attribute__((aligned(16))) float cfw[NWV][ROWS];  // each wave's rescale factors
 #pragma unroll
     for (int k = 0; k < QI; k++) {
@@ -150,6 +171,14 @@ __global__ void __launch_bounds__(NTH, NWV == 4 ? 2 : 1) attn_f32(const float* _
         *(half8*)&ql[row][d8] = lo;
     }
     __syncthreads();
+    if (nr > 0) {  // every wave's direct loads have landed: each waited for its own Q, loaded after them
+        for (int i = tid; i < nr * HD; i += NTH) {
+            const int r = i / HD, d = i % HD;
+            newk[r][d] = rope_dim(ain + r * HD, ain + 8 * HD + r * 64, d);
+            newv[r][d] = ain[(4 + r) * HD + d];
+        }
+        __syncthreads();
+    }
 
     const int vis = n + t0 + (r32 >> 3);  // lane's row sees keys < vis (and of this split, < hi)
     float m_run = NEG_INF, l_run = 0.f;
