@@ -42,8 +42,8 @@ using mkv::hip_fail;
 // Scratch of mkv_append_decode_noalloc: the split-K partials of one decode (2 kv heads x 32 rows x up to 248 splits x
 // 260 floats = 16,506,880 bytes), a file-scope device array instead of the handle's workspace, so that the call
 // allocates nothing. Each GPU holds its own copy until the process ends. Host code never uses the array's name as a
-// device address: its per-device address comes from hipGetSymbolAddress, resolved once per device by mkv_create
-// with that device current. Every call on one GPU shares it; calls that overlap on one GPU (other streams, other
+// device address: its per-device address comes from hipGetSymbolAddress, resolved once per device with that device
+// current, by mkv_create (whose other work does not depend on it) or else by the entry point's first call there. Every call on one GPU shares it; calls that overlap on one GPU (other streams, other
 // handles) race. No part needs clearing: a decode reads only partials its own core launch wrote.
 constexpr int SCRATCH_CHUNKS = 248;
 constexpr size_t SCRATCH_FLOATS = (size_t)KVH * ROWS * SCRATCH_CHUNKS * PART;
