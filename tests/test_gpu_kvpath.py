@@ -196,7 +196,8 @@ def test_decode_split_count_sequence(torch_gpu, mk):
 
 @pytest.mark.parametrize("ctx,n0,ntok,start", [(4096, 300, 4, 0), (4096, 1000, 1, 0), (8192, 5000, 4, 17),
                                                (4096, 2, 1, 0), (4096, 129, 2, 0), (20480, 19000, 3, 0),
-                                               (20480, 19001, 4, 12345), (8192, 40, 4, 33)])
+                                               (20480, 19001, 4, 12345), (8192, 40, 4, 33),
+                                               (4096, 4093, 4, 0), (4096, 4096, 1, 0)])  # up to the context's end
 def test_decode_f32(torch_gpu, mk, ctx, n0, ntok, start):
     torch = torch_gpu
     print(f"decode f32 ctx={ctx} n0={n0} ntok={ntok}", flush=True)
@@ -287,7 +288,8 @@ def test_append_decode_fused_entry(torch_gpu, mk, ctx, n0, fmt):
 
 @pytest.mark.parametrize("n0,T,start", [(2000, 64, 0), (100, 512, 0), (3000, 37, 0), (1, 16, 0), (2500, 96, 300),
                                         (3000, 63, 0), (1, 1, 0), (2001, 8, 0), (1000, 32, 0), (3500, 5, 0),
-                                        (3000, 29, 1234), (60, 2, 0), (2000, 64, 700)])
+                                        (3000, 29, 1234), (60, 2, 0), (2000, 64, 700),
+                                        (3585, 512, 0), (4090, 7, 0), (4033, 64, 1000)])  # the last three end at ctx
 def test_prefill_f16(torch_gpu, mk, n0, T, start):
     """Blocks of 64 tokens or more against attn_fa_mx (f16 Q), smaller blocks against attn_fd4 (f32 Q) at 1e-5."""
     torch = torch_gpu
@@ -305,7 +307,8 @@ def test_prefill_f16(torch_gpu, mk, n0, T, start):
 
 
 @pytest.mark.parametrize("n0,T,start", [(1500, 70, 0), (100, 512, 0), (2500, 96, 300), (1, 16, 0), (3000, 5, 0),
-                                        (40, 3, 0), (3500, 512, 2900), (1500, 70, 400)])
+                                        (40, 3, 0), (3500, 512, 2900), (1500, 70, 400),
+                                        (3585, 512, 0), (4092, 5, 0)])  # the last two end at ctx
 def test_prefill_f32(torch_gpu, mk, n0, T, start):
     torch = torch_gpu
     print(f"prefill f32 n0={n0} T={T} start={start}", flush=True)
