@@ -94,7 +94,7 @@ def test_rope_bit_exact(torch_gpu, mf):
 # (fmt, sliding, ctx, pos): one token at pos, after positions [0, pos] were written
 DECODE = [(F32, False, 4096, 3000), (F16, False, 4096, 777), (F32, True, 4096, 2500), (F16, True, 4096, 1100),
           (F32, True, 4096, 100), (F32, False, 40960, 40000), (F16, False, 40960, 32768), (F32, False, 4096, 0),
-          (F16, True, 8192, 5000)]
+          (F16, True, 8192, 5000), (F16, False, 4096, 4095), (F32, False, 4096, 4095)]  # the last two: ctx's last row
 
 
 @pytest.mark.parametrize("fmt,sliding,ctx,pos", DECODE)
@@ -118,7 +118,8 @@ PREFILL = [(F32, False, 4096, 200, 70), (F16, False, 4096, 0, 9), (F32, True, 40
            (F32, True, 4096, 2000, 2), (F16, False, 8192, 5000, 2), (F32, False, 4096, 1000, 3), (F16, True, 4096, 1500, 4),
            (F32, False, 40960, 39000, 2), (F16, True, 8192, 5000, 512), (F16, True, 4096, 1037, 100),
            (F16, False, 40960, 39000, 257), (F16, False, 4096, 31, 63), (F16, False, 40960, 30000, 8),
-           (F32, False, 40960, 30001, 12), (F16, True, 40960, 30002, 29)]
+           (F32, False, 40960, 30001, 12), (F16, True, 40960, 30002, 29),
+           (F16, False, 4096, 3584, 512), (F32, False, 4096, 4092, 4), (F16, False, 4096, 4094, 2)]  # up to ctx's end
 
 
 @pytest.mark.parametrize("fmt,sliding,ctx,pos0,T", PREFILL)
