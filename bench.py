@@ -21,6 +21,7 @@ during a second pass of the same K steps). cpu_baseline = the C restatement in o
 only as the reported CPU baseline) timed on this host's cores on the same cache.
 """
 import argparse
+import functools
 import json
 import os
 import sys
@@ -72,6 +73,52 @@ def parse():
 TRAFFIC = {"decode_f16": 142.52e6, "prefill_f16": 163.27e6}
 
 
+def demangle_nested(raw):
+    """The qualified name and integer/bool template arguments of an Itanium-mangled nested name (_ZN...E), the form
+    of this library's kernels; rocprofv3 leaves a name mangled when its demangler does not know an argument type
+    (_Float16, DF16_). None for any other form."""
+    import re
+    if not raw.startswith("_ZN"):
+        return None
+    i, parts, targs = 3, [], ""
+    while i < len(raw) and raw[i].isdigit():
+        m = re.match(r"\d+", raw[i:])
+        n = int(m.group())
+        i += len(m.group())
+        ident = raw[i:i + n]
+        i += n
+        if not ident.startswith("_GLOBAL__N"):  # the anonymous namespace
+            parts.append(ident)
+    if not parts:
+        return None
+    if raw[i:i + 1] == "I":  # template arguments: literals L<type><value>E
+        args, i = [], i + 1
+        while raw[i:i + 1] == "L":
+            m = re.match(r"L([a-z])(n?\d+)E", raw[i:])
+            if not m:
+                return None
+            t, v = m.groups()
+            v = v.replace("n", "-")
+            args.append(("true" if v == "1" else "false") if t == "b" else v)
+            i += len(m.group())
+        if raw[i:i + 1] != "E":
+            return None
+        targs = "<" + ", ".join(args) + ">"
+    return "::".join(parts) + targs
+
+
+@functools.lru_cache(maxsize=None)
+def short_name(raw, width=90):
+    """A kernel name of a rocprofv3 csv without namespaces' noise or arguments (mangled names demangled first)."""
+    raw = demangle_nested(raw) or raw
+    return raw.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:width]
+
+
+def library_kernel(name):
+    """This library's kernels and the probe's (not torch's or the runtime's)."""
+    return "mkv" in name or name.startswith("probe_")
+
+
 def counter_summary(d):
     """Mean value per dispatch of each collected counter, per (kernel, grid) of a rocprofv3 --pmc directory."""
     import csv
@@ -80,8 +127,8 @@ def counter_summary(d):
     f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)[0]
     per = collections.defaultdict(lambda: collections.defaultdict(list))
     for r in csv.DictReader(open(f)):
-        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:60]
-        if "mkv" not in name:
+        name = short_name(r["Kernel_Name"], 60)
+        if not library_kernel(name):
             continue
         per[(name, int(r["Grid_Size"]))][r["Counter_Name"]].append(float(r["Counter_Value"]))
     names = sorted({c for v in per.values() for c in v})
@@ -100,7 +147,9 @@ def trace_summary(path):
     import statistics
     per = collections.defaultdict(list)
     for r in csv.DictReader(open(path)):
-        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:90]
+        name = short_name(r["Kernel_Name"])
+        if not library_kernel(name):
+            continue
         key = (name, r.get("Grid_Size_X", r.get("Grid_Size")), r.get("Workgroup_Size_X", r.get("Workgroup_Size")))
         per[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000)
     print("| kernel | grid threads | wg | launches | mean us | median us | min us | max us |")
@@ -139,8 +188,7 @@ def pmc_summary(fetch_dir, write_dir):
             continue
         fk, wk = sum(fetch[key]) / len(fetch[key]), sum(write[key]) / len(write[key])
         rb, wb = fk * 1024 * f_scale / 1e6, wk * 1024 * w_scale / 1e6
-        short = name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
-        short = short.replace("mkv::flint::", "").replace("mkv::", "")[:48]
+        short = short_name(name, 1000).replace("mkv::flint::", "").replace("mkv::", "")[:48]
         print(f"| {short} | {grid} | {len(fetch[key])} | {fk:.1f} | {wk:.1f} | {rb:.2f} | {wb:.2f} | {rb + wb:.2f} |")
 
 

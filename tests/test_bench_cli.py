@@ -41,15 +41,22 @@ def test_trace_summary(tmp_path):
     rows.append({"Kernel_Name": "void mkv::(anonymous namespace)::decode_f16<false>(_Float16 const*)",
                  "Grid_Size_X": "55296", "Workgroup_Size_X": "512", "Start_Timestamp": "100",
                  "End_Timestamp": "24600"})
+    # a name the trace left mangled (decode_f16<true>), and a torch kernel, which is left out
+    rows.append({"Kernel_Name": "_ZN3mkv12_GLOBAL__N_110decode_f16ILb1EEEvPDF16_S2_mPKfiiifiiPfS4_S4_S4_iiii", "Grid_Size_X": "33792",
+                 "Workgroup_Size_X": "512", "Start_Timestamp": "0", "End_Timestamp": "6500"})
+    rows.append({"Kernel_Name": "void at::native::vectorized_elementwise_kernel<4>(int)", "Grid_Size_X": "64",
+                 "Workgroup_Size_X": "64", "Start_Timestamp": "0", "End_Timestamp": "90000"})
     f = tmp_path / "run_kernel_trace.csv"
     write_csv(str(f), rows)
     r = run("--trace-summary", str(f))
     assert r.returncode == 0, r.stderr
     t = table_rows(r.stdout)
+    assert len(t) == 3
     # ordered by total time: the decode (24.5 us) before the three merges (12 us in all)
     assert t[0][:4] == ["mkv::decode_f16<false>", "55296", "512", "1"] and t[0][4] == "24.50"
     assert t[1][:4] == ["mkv::decode_combine<9, false>", "16384", "256", "3"]
     assert t[1][4:] == ["4.00", "4.00", "3.00", "5.00"]  # mean, median, min, max
+    assert t[2][:5] == ["mkv::decode_f16<true>", "33792", "512", "1", "6.50"]
 
 
 def pmc_dir(root, counter, values):
