@@ -235,7 +235,7 @@ def queue_ahead(torch, us=40.0):
     region's start event: the GPU is then busy while the host submits the region's first launches, so the region
     starts with them already queued instead of counting the host's submission of the first launch (about 8 us on an
     idle GPU, 0.4 us per step at 20 cfg2 steps). Nothing of the timed work moves out of the region."""
-    if "cycles" not in _SPIN:
+    if "per_us" not in _SPIN:  # spin cycles per microsecond
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         n, t = 200000, 0.0
         for _ in range(2):  # the first launch of the spin kernel is not representative
@@ -245,8 +245,8 @@ def queue_ahead(torch, us=40.0):
             b.record()
             torch.cuda.synchronize()
             t = a.elapsed_time(b) * 1000
-        _SPIN["cycles"] = max(1000, min(int(n * us / max(t, 1e-3)), 1 << 30))
-    torch.cuda._sleep(_SPIN["cycles"])
+        _SPIN["per_us"] = n / max(t, 1e-3)
+    torch.cuda._sleep(max(1000, min(int(_SPIN["per_us"] * us), 1 << 30)))
 
 
 def bench_decode(torch, mk, steps, warmup):
