@@ -38,7 +38,9 @@ namespace {
 #define FL_FUSE_NCH 8     // decode with the merge fused (short spans): splits per kv head at most
 #endif
 #ifndef FL_FUSE_SPLIT
-#define FL_FUSE_SPLIT 64  // decode with the merge fused: positions per split at least
+#define FL_FUSE_SPLIT 80  // decode with the merge fused: positions per split at least (a sliding layer's 513-position
+                          // window: 6 splits; against 8 / 7 / 5 / 4 splits 9.8 against 10.7 / 9.8 / 10.0 / 10.7 us per
+                          // f32 call, 8.6 against 8.8 / 8.6 / 8.5 / 8.8 us per f16 call)
 #endif
 #ifndef FL_FUSE_SPAN
 #define FL_FUSE_SPAN 2048  // decode: spans up to this many positions merge in the kernel
