@@ -35,7 +35,7 @@ struct Plan {
 };
 constexpr int WS_ROWS = 16384;  // rows x splits per kv head that the split partials hold
 constexpr int WS_ARRIVALS = 64;  // floats after the partials: the fused decode's arrival counters (zero at creation)
-Plan plan(int pos0, int T, int win);
+Plan plan(int fmt, int pos0, int T, int win);
 size_t ws_floats();  // split partials of any plan (4 kv heads x WS_ROWS x PART) and the arrival counters
 
 hipError_t launch_attn(int fmt, const void* kp, const void* vp, int rows, const float* q, int T, int pos0, int win,

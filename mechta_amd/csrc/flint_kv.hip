@@ -38,12 +38,20 @@ namespace {
 #define FL_FUSE_NCH 8     // decode with the merge fused (short spans): splits per kv head at most
 #endif
 #ifndef FL_FUSE_SPLIT
-#define FL_FUSE_SPLIT 80  // decode with the merge fused: positions per split at least (a sliding layer's 513-position
-                          // window: 6 splits; against 8 / 7 / 5 / 4 splits 9.8 against 10.7 / 9.8 / 10.0 / 10.7 us per
-                          // f32 call, 8.6 against 8.8 / 8.6 / 8.5 / 8.8 us per f16 call)
+#define FL_FUSE_SPLIT 80  // decode with the merge fused: positions per split at least (at 544 positions: 6 splits;
+                          // against 8 / 7 / 5 / 4 splits 9.8 against 10.7 / 9.8 / 10.0 / 10.7 us per f32 call, 8.6
+                          // against 8.8 / 8.6 / 8.5 / 8.8 us per f16 call)
 #endif
-#ifndef FL_FUSE_SPAN
-#define FL_FUSE_SPAN 2048  // decode: spans up to this many positions merge in the kernel
+// Decodes of spans up to these many positions merge in the kernel; longer ones launch the merge. One token on a full
+// layer, us per call with the merge in the kernel against two launches: f32 at 320 / 384 / 448 / 512 / 768 / 2,048
+// positions 9.1 / 9.5 / 10.1 / 10.2 / 10.4 / 13.0 against 9.0 / 9.5 / 9.8 / 9.9 / 9.6 / 10.7; f16 8.1 / 8.3 / 8.6 / 8.8
+// / 9.0 / 10.4 against 8.2 / 8.6 / 8.8 / 9.0 / 8.7 / 9.2; at 256 positions 9.0 / 8.2 against 10.7 / 10.2 (f32 / f16).
+// A sliding layer's 513-544 positions: 9.8 / 8.6 against 8.9 / 8.3.
+#ifndef FL_FUSE_SPAN_F32
+#define FL_FUSE_SPAN_F32 384
+#endif
+#ifndef FL_FUSE_SPAN_F16
+#define FL_FUSE_SPAN_F16 512
 #endif
 
 constexpr int TILE = 32;
@@ -1035,13 +1043,14 @@ __global__ void __launch_bounds__(256) fl_merge_few(const float* __restrict__ pa
 
 }  // namespace
 
-Plan plan(int pos0, int T, int win) {
+Plan plan(int fmt, int pos0, int T, int win) {
     const int lo0 = win > 0 && pos0 + 1 > win ? pos0 + 1 - win : 0;
     const int klo = lo0 / 32 * 32, span = pos0 + T - klo;
     int nrb = (T + 3) / 4;
     int nch;
     int fused = 0;
-    if (T <= 2 && span <= FL_FUSE_SPAN) {  // fl_dec16 merging its own partials: splits of at least FL_FUSE_SPLIT
+    if (T <= 2 && span <= (fmt == 1 ? FL_FUSE_SPAN_F32 : FL_FUSE_SPAN_F16)) {  // fl_dec16 merging its own partials:
+                                                                              // splits of at least FL_FUSE_SPLIT
         nch = span / FL_FUSE_SPLIT;
         nch = nch > FL_FUSE_NCH ? FL_FUSE_NCH : nch;
         fused = 1;

@@ -155,7 +155,7 @@ int mfl_attend(mfl_t* h, int layer, int pos0, int ntok, const float* q, const fl
         return fail(MKV_E_POS, "mfl_attend: positions [%d, %d) outside the context %d", pos0, pos0 + ntok, h->ctx);
     const int rows = h->rows[layer];
     const int win = h->swa[layer] ? MFL_WINDOW : 0;
-    const fl::Plan p = fl::plan(pos0, ntok, win);
+    const fl::Plan p = fl::plan(h->fmt, pos0, ntok, win);
     hipError_t e = fl::launch_attn(h->fmt, plane(h, layer, 0), plane(h, layer, 1), rows, q, ntok, pos0, win, p,
                                    h->ws, sinks, out, h->stream);
     return e == hipSuccess ? MKV_OK : hip_fail(e, "mfl_attend");

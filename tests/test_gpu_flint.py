@@ -94,7 +94,10 @@ def test_rope_bit_exact(torch_gpu, mf):
 # (fmt, sliding, ctx, pos): one token at pos, after positions [0, pos] were written
 DECODE = [(F32, False, 4096, 3000), (F16, False, 4096, 777), (F32, True, 4096, 2500), (F16, True, 4096, 1100),
           (F32, True, 4096, 100), (F32, False, 40960, 40000), (F16, False, 40960, 32768), (F32, False, 4096, 0),
-          (F16, True, 8192, 5000), (F16, False, 4096, 4095), (F32, False, 4096, 4095)]  # the last two: ctx's last row
+          (F16, True, 8192, 5000), (F16, False, 4096, 4095), (F32, False, 4096, 4095),  # these two: ctx's last row
+          # either side of the spans whose decode merges in the kernel (f32 up to 384 positions, f16 up to 512)
+          (F32, False, 4096, 383), (F32, False, 4096, 384), (F16, False, 4096, 300), (F16, False, 4096, 511),
+          (F16, False, 4096, 512)]
 
 
 @pytest.mark.parametrize("fmt,sliding,ctx,pos", DECODE)
