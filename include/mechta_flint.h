@@ -14,8 +14,8 @@
  * f32 operands split into f16 hi + lo (hi.hi + hi.lo + lo.hi, f32 accumulation; within 1e-5 of exact f32). mfl_read_rows /
  * mfl_write_rows convert to and from the reference's row layout [row][kvh][128] (flint_attn.wgsl:3, kv_put).
  *
- * All calls are ordered on the handle's stream; device pointers are plain HIP device addresses. A one-token decode over a
- * short span merges its split partials in the kernel, through per-kv-head arrival counters the handle keeps: two such
+ * All calls are ordered on the handle's stream; device pointers are plain HIP device addresses. A decode of 1-2 tokens
+ * over a short span (up to 384 positions on an f32 cache, 512 on an f16 one) merges its split partials in the kernel, through per-kv-head arrival counters the handle keeps: two such
  * decodes of one handle must not run at once, so keep every call of a handle on one stream (mfl_set_stream moves them
  * all).
  */
