@@ -642,6 +642,85 @@ def bench_flint(torch, mk, ctx=32768):
     return res
 
 
+def bench_producer(torch, mk):
+    """The q/k producer (mkv_qk_norm_rope: rmsnorm of q and k, rope2 of q) for the cfg2 step's 4 tokens and cfg3's 512,
+    called through the C ABI. Bytes per token: qf 32 KB and kb 2 KB read (f32), q 16 KB and k 2 KB written, the table
+    row 256 B; the norm weights once."""
+    import ctypes
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2040)
+    st = mk.KvStore(1, 32768, mk.F16)
+    lib, h, P = mk.lib(), st.handle, ctypes.c_void_p
+    res = {}
+    qw, kw = seeded_normal(torch, gen, (256,)), seeded_normal(torch, gen, (256,))
+    for name, ntok, pos, it in (("cfg2_4_tokens", 4, 28000, 200), ("cfg3_512_tokens", 512, 28000, 50)):
+        qf, kb = seeded_normal(torch, gen, (ntok, 16, 512)), seeded_normal(torch, gen, (ntok, 2, 256))
+        qo, ko = torch.empty((ntok, 16, 256), device="cuda"), torch.empty((ntok, 2, 256), device="cuda")
+        a = [P(x.data_ptr()) for x in (qf, kb, qw, kw, qo, ko)]
+
+        def f():
+            rc = lib.mkv_qk_norm_rope(h, pos, ntok, a[0], a[1], a[2], a[3], ctypes.c_float(1e-6), a[4], a[5])
+            if rc != 0:
+                raise mk.MkvError(rc, lib.mkv_last_error().decode())
+        warm(torch, f, ms=20.0)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        queue_ahead(torch)
+        e0.record()
+        for _ in range(it):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / it * 1000
+        nbytes = ntok * (8192 + 512 + 4096 + 512 + 64) * 4 + 2 * 256 * 4
+        res[name] = {"us": round(us, 2), "bytes": nbytes, "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    st.close()
+    return res
+
+
+def bench_root(torch, mk, layers=10, p=8192):
+    """A root file of positions [0, p) of a 10-layer f16 store (the reference's MECHTA-ROOT-1 container): save
+    (gather to host memory, write path.tmp, rename), the same with the write on the handle's thread (the call's
+    return, then the wait), and load, in MB/s of the file's bytes. Written under the system's temporary directory
+    and removed afterwards; disk and page cache set the rate, not HBM."""
+    import tempfile
+    import numpy as np
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2041)
+    st = mk.KvStore(layers, p, mk.F16)
+    tabs = rope_tabs(torch, mk, 0, p)
+    for layer in range(layers):
+        fill_store(torch, mk, st, layer, p, gen, tabs)
+    tokens = np.arange(p, dtype=np.uint32)
+    d = tempfile.mkdtemp(prefix="mkv_root_bench_")
+    path = os.path.join(d, "root.bin")
+    res = {"p": p, "layers": layers}
+    try:
+        st.root_save(path, p, tokens)  # once untimed: the first host copy of a process pays a set-up
+        t0 = time.perf_counter()
+        st.root_save(path, p, tokens)
+        t_save = time.perf_counter() - t0
+        size = os.path.getsize(path)
+        t0 = time.perf_counter()
+        st.root_save(path, p, tokens, background=True)
+        t_ret = time.perf_counter() - t0
+        st.root_wait()
+        t_bg = time.perf_counter() - t0
+        st.set_len(0)
+        t0 = time.perf_counter()
+        st.root_load(path)
+        t_load = time.perf_counter() - t0
+        res.update({"file_mb": round(size / 1e6, 1), "save_mbps": round(size / t_save / 1e6, 1),
+                    "background_return_ms": round(t_ret * 1e3, 2), "background_total_ms": round(t_bg * 1e3, 2),
+                    "load_mbps": round(size / t_load / 1e6, 1)})
+    finally:
+        for f in os.listdir(d):
+            os.remove(os.path.join(d, f))
+        os.rmdir(d)
+        st.close()
+    return res
+
+
 def bench_read_floor(torch, nbytes, nbuf=10, reps=60):
     """A plain streaming read of nbytes by one launch (libmkv_probe.so: 248 work-groups, 64 KB stages dealt round
     robin, non-temporal 16-byte loads, two stages in flight), over nbuf different buffers in turn so that nothing
@@ -1034,6 +1113,8 @@ def main():
         res["cfg4_kv_read_gbps"] = round(gbs4, 1)
         res["cfg5"] = bench_cfg5(torch, mk)
         res["flint"] = bench_flint(torch, mk)
+        res["producer"] = bench_producer(torch, mk)
+        res["root"] = bench_root(torch, mk)
         res["hbm_read_floor"] = bench_read_floor(torch, int(core_bytes))
         res["mfma_sustained"] = bench_mfma_rate()
     if args.calib_copy:
