@@ -59,6 +59,9 @@ def parse():
                     help="only the Flint KV path's figures (decode and prefill, full and sliding layers), one JSON line")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only the sustained dense f16 MFMA rate of the part (libmkv_probe.so), one JSON line")
+    ap.add_argument("--token-sweep", action="store_true",
+                    help="only plain decodes of 1 to 4 tokens at 65,536 positions, with and without a window start, "
+                         "one JSON line")
     ap.add_argument("--cfg5-only", action="store_true",
                     help="only configs[4] (f32 store: snapshot, restore, verify, prefill), as one JSON line (profiling)")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
@@ -728,6 +731,43 @@ def bench_root(torch, mk, layers=10, p=8192):
     return res
 
 
+def bench_token_counts(torch, mk, n0=65536, layers=6):
+    """Plain decodes (mkv_decode, no append) of 1 to 4 tokens at n0 positions, with and without a window start, the
+    layers rotated (f16, more bytes than the last-level cache), us per call through the C ABI."""
+    import ctypes
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2042)
+    st = mk.KvStore(layers, (n0 + 4 + 1023) // 1024 * 1024, mk.F16)
+    tabs = rope_tabs(torch, mk, 0, n0)
+    for layer in range(layers):
+        fill_store(torch, mk, st, layer, n0, gen, tabs)
+    lib, h, P = mk.lib(), st.handle, ctypes.c_void_p
+    res = {}
+    for nt in (1, 2, 3, 4):
+        for start in (0, 3000):
+            q = seeded_normal(torch, gen, (nt, 16, 256))
+            out = torch.empty((nt, 16, 256), device="cuda")
+            pq, po = P(q.data_ptr()), P(out.data_ptr())
+            i = [0]
+
+            def f():
+                rc = lib.mkv_decode(h, i[0] % layers, pq, nt, n0 - nt + 1, start, 1.0 / 16, po, None)
+                if rc != 0:
+                    raise mk.MkvError(rc, lib.mkv_last_error().decode())
+                i[0] += 1
+            warm(torch, f, ms=30.0)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            queue_ahead(torch)
+            e0.record()
+            for _ in range(60):
+                f()
+            e1.record()
+            torch.cuda.synchronize()
+            res[f"{nt}_tokens_start_{start}_us"] = round(e0.elapsed_time(e1) / 60 * 1000, 2)
+    st.close()
+    return {"positions": n0, "layers": layers, **res}
+
+
 def bench_read_floor(torch, nbytes, nbuf=10, reps=60):
     """A plain streaming read of nbytes by one launch (libmkv_probe.so: 248 work-groups, 64 KB stages dealt round
     robin, non-temporal 16-byte loads, two stages in flight), over nbuf different buffers in turn so that nothing
@@ -1048,6 +1088,9 @@ def main():
         return
     if args.mfma_probe:
         print(json.dumps({"mfma_sustained": bench_mfma_rate()}), flush=True)
+        return
+    if args.token_sweep:
+        print(json.dumps({"token_sweep": bench_token_counts(torch, mk)}), flush=True)
         return
     if args.cfg5_only:
         r = bench_cfg5(torch, mk)
