@@ -122,7 +122,8 @@ PREFILL = [(F32, False, 4096, 200, 70), (F16, False, 4096, 0, 9), (F32, True, 40
            (F32, False, 40960, 39000, 2), (F16, True, 8192, 5000, 512), (F16, True, 4096, 1037, 100),
            (F16, False, 40960, 39000, 257), (F16, False, 4096, 31, 63), (F16, False, 40960, 30000, 8),
            (F32, False, 40960, 30001, 12), (F16, True, 40960, 30002, 29),
-           (F16, False, 4096, 3584, 512), (F32, False, 4096, 4092, 4), (F16, False, 4096, 4094, 2)]  # up to ctx's end
+           (F16, False, 4096, 3584, 512), (F32, False, 4096, 4092, 4), (F16, False, 4096, 4094, 2),  # up to ctx's end
+           (F16, False, 4096, 200, 2), (F32, False, 4096, 100, 2)]  # two tokens merged in the kernel (short spans)
 
 
 @pytest.mark.parametrize("fmt,sliding,ctx,pos0,T", PREFILL)
