@@ -59,6 +59,8 @@ def parse():
                     help="only the Flint KV path's figures (decode and prefill, full and sliding layers), one JSON line")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only the sustained dense f16 MFMA rate of the part (libmkv_probe.so), one JSON line")
+    ap.add_argument("--side-only", action="store_true",
+                    help="only the q/k producer and root-file figures of the default line, one JSON line (profiling)")
     ap.add_argument("--token-sweep", action="store_true",
                     help="only plain decodes of 1 to 4 tokens at 65,536 positions, with and without a window start, "
                          "one JSON line")
@@ -1088,6 +1090,9 @@ def main():
         return
     if args.mfma_probe:
         print(json.dumps({"mfma_sustained": bench_mfma_rate()}), flush=True)
+        return
+    if args.side_only:
+        print(json.dumps({"producer": bench_producer(torch, mk), "root": bench_root(torch, mk)}), flush=True)
         return
     if args.token_sweep:
         print(json.dumps({"token_sweep": bench_token_counts(torch, mk)}), flush=True)
