@@ -681,7 +681,7 @@ def producer_inputs(seed, ntok):
             r.uniform(0.5, 1.5, 256).astype(np.float32), r.uniform(0.5, 1.5, 256).astype(np.float32))
 
 
-@pytest.mark.parametrize("pos,ntok", [(0, 1), (4096, 1), (65532, 4), (1000, 512), (66000, 37)])
+@pytest.mark.parametrize("pos,ntok", [(0, 1), (4096, 1), (65532, 4), (1000, 512), (66000, 37), (66556, 4)])
 def test_qk_norm_rope_bit_exact(torch_gpu, mk, pos, ntok):
     """The producer (rmsnorm of q and k, rope2 of q) bit-identical to the oracle's restatement, with the device
     RoPE rows bit-identical to rope_table."""
