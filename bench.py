@@ -252,8 +252,9 @@ def queue_ahead(torch, us=40.0):
             b.record()
             torch.cuda.synchronize()
             t = a.elapsed_time(b) * 1000
-        _SPIN["per_us"] = n / max(t, 1e-3)
-    torch.cuda._sleep(max(1000, min(int(_SPIN["per_us"] * us), 1 << 30)))
+        _SPIN["per_us"] = n / t if t > 1.0 else 0.0  # a spin shorter than 1 us: not calibrated, no spin
+    if _SPIN["per_us"] > 0:
+        torch.cuda._sleep(max(1000, min(int(_SPIN["per_us"] * us), 4 << 20)))  # at most 4M cycles
 
 
 def bench_decode(torch, mk, steps, warmup):
